@@ -1,0 +1,90 @@
+"""ctypes binding of libegpt_hip.so (the C ABI declared in include/egpt.h).
+
+torch is imported first so the library binds to the HIP runtime torch already
+loaded (both carry the SONAME libamdhip64.so.7): one runtime, one set of device
+pointers and streams. There is no fallback: a missing or stale library raises.
+"""
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / 'libegpt_hip.so'
+
+EGPT_OK = 0
+EGPT_F32, EGPT_BF16, EGPT_F16 = 0, 1, 2
+ABI_VERSION = 1
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_vp = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+_c_f = ctypes.c_float
+
+# name -> (restype, argtypes); the full exported surface of include/egpt.h
+SIGNATURES = {
+    'egpt_abi_version': (_c_int, []),
+    'egpt_status_string': (ctypes.c_char_p, [_c_int]),
+    'egpt_int8_gemv': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp]),
+    'egpt_int8_gemv_splitk_workspace': (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
+    'egpt_int8_gemv_splitk': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
+                                       _c_int, _c_vp, _c_size, _c_vp]),
+    'egpt_decode_attn_default_splits': (_c_int, [_c_int, _c_int, _c_int]),
+    'egpt_decode_attn_workspace': (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
+    'egpt_decode_attn': (_c_int, [_c_int,
+                                  _c_vp, _c_i64, _c_i64,
+                                  _c_vp, _c_i64, _c_i64, _c_i64,
+                                  _c_vp, _c_i64, _c_i64, _c_i64,
+                                  _c_vp, _c_i64,
+                                  _c_vp, _c_i64, _c_i64,
+                                  _c_vp, _c_size,
+                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp]),
+}
+
+_lib = None
+
+
+class EgptError(RuntimeError):
+    """A libegpt_hip entry point returned a non-zero status."""
+
+    def __init__(self, name, status):
+        self.status = status
+        msg = lib().egpt_status_string(status).decode() if _lib is not None else str(status)
+        super().__init__(f'{name} failed: {msg} ({status})')
+
+
+def lib():
+    """The loaded library, with argtypes set. Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.is_file():
+            raise ImportError(f'{LIB_PATH} is not built: run `python -m efficientgpt_amd._build` '
+                              '(or __graft_entry__.build())')
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        got = handle.egpt_abi_version()
+        if got != ABI_VERSION:
+            raise ImportError(f'{LIB_PATH} has ABI {got}, expected {ABI_VERSION}: rebuild it')
+        _lib = handle
+    return _lib
+
+
+def check(name, status):
+    if status != EGPT_OK:
+        raise EgptError(name, status)
+
+
+def stream_ptr(device=None):
+    """The raw hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype):
+    try:
+        return {torch.float32: EGPT_F32, torch.bfloat16: EGPT_BF16, torch.float16: EGPT_F16}[dtype]
+    except KeyError:
+        raise ValueError(f'unsupported dtype {dtype}') from None

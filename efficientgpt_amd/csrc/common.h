@@ -1,0 +1,136 @@
+// Device helpers shared by the gfx950 decode kernels: bf16/fp16 packing, DPP
+// reductions over 64-wide wavefronts, 16-byte vector loads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/egpt.h"
+
+namespace egpt {
+
+constexpr int kWave = 64;
+
+// Native 4 x 32-bit vector: one 16-byte global load (global_load_dwordx4).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950; NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// Element traits for the attention kernels: storage type -> fp32 and back.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* out) {
+    out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
+    out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
+  }
+  __device__ static __forceinline__ float load1(const void* p) { return *(const float*)p; }
+  __device__ static __forceinline__ void store1(void* p, float f) { *(float*)p = f; }
+};
+template <> struct Elem<__bf16> {
+  static constexpr int kBytes = 2;
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* out) {
+    out[0] = bf16_lo(v.x); out[1] = bf16_hi(v.x); out[2] = bf16_lo(v.y); out[3] = bf16_hi(v.y);
+    out[4] = bf16_lo(v.z); out[5] = bf16_hi(v.z); out[6] = bf16_lo(v.w); out[7] = bf16_hi(v.w);
+  }
+  __device__ static __forceinline__ float load1(const void* p) { return bf16_to_f32(*(const uint16_t*)p); }
+  __device__ static __forceinline__ void store1(void* p, float f) { *(uint16_t*)p = f32_to_bf16(f); }
+};
+template <> struct Elem<_Float16> {
+  static constexpr int kBytes = 2;
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* out) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffffu));
+      out[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+    }
+  }
+  __device__ static __forceinline__ float load1(const void* p) { return f16_to_f32(*(const uint16_t*)p); }
+  __device__ static __forceinline__ void store1(void* p, float f) { *(uint16_t*)p = f32_to_f16(f); }
+};
+
+// ---------------------------------------------------------------- loads
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+
+// Streaming load for data read exactly once (weights): non-temporal hint keeps it
+// from evicting the small, re-read operands (activations, scales) from L2.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+// ---------------------------------------------------------------- DPP reductions
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+
+// Sum over aligned groups of N lanes (N in 1,2,4,8,16,32,64); every lane of a
+// group receives the group's total. The summation order is fixed, so results
+// are bitwise reproducible run to run.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += dpp<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, dpp<kDppXor1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<kDppXor2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
+  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+// Whole-wavefront sum, returned as a wave-uniform value: 16-lane DPP butterflies
+// then the four row totals read out of lanes 0/16/32/48.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group_sum<16>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = group_max<16>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+}  // namespace egpt
+
+// Map a HIP launch result to the library's status convention.
+#define EGPT_LAUNCH_STATUS() (hipGetLastError() == hipSuccess ? EGPT_OK : EGPT_ERR_LAUNCH)

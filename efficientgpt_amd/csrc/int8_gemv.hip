@@ -1,0 +1,300 @@
+// Weight-only int8 GEMV for batch-1 decode on gfx950 (MI355X).
+//
+//   y[m, n] = bf16( scale[n] * sum_k x[m, k] * w[n, k] ),   M <= 16
+//
+// Same arithmetic contract as the reference's Triton _dot16 kernel
+// (research/realmodel/int8_linear.py:26-38): int8 weights are exact in the
+// multiplier's input format, products and sums are fp32, the per-channel scale
+// multiplies the finished fp32 sum, and the result is rounded once to bf16.
+//
+// Design (memory-bound: ~1 byte of weight per 2 flops at M = 1):
+//   * A block is 4 wavefronts; each wavefront owns R consecutive output rows and
+//     streams them with 16-byte loads per lane, so one load instruction moves
+//     1 KiB of a row (64 lanes x 16 int8). Rows are [N, K] row-major, the
+//     nn.Linear layout, so a block reads one contiguous 4*R*K byte span.
+//   * Dequantisation stays in registers: each int8 byte is biased to unsigned
+//     (xor 0x80) and converted with one v_cvt_f32_ubyteN, multiplied by the fp32
+//     activation with one FMA; the bias (128 * sum x) is removed once per lane.
+//     Every product is exact in fp32 (8-bit x 8-bit significands).
+//   * Activations are re-read per 1 KiB chunk from L1/L2 (a few KiB, shared by
+//     every block), so register use does not grow with K.
+//   * The row sum is a DPP butterfly over 16 lanes plus four readlanes: a fixed
+//     summation order, so results are bitwise reproducible.
+//   * The scale is applied after the reduction, then one bf16 rounding.
+#include "common.h"
+
+namespace egpt {
+namespace {
+
+constexpr int kGemvWaves = 4;
+constexpr int kGemvThreads = kGemvWaves * kWave;
+constexpr int kChunk = kWave * 16;  // int8 elements covered by one 16-byte load per lane
+
+enum { kEpiStore = 0, kEpiPartial = 1 };
+
+// 16 int8 weights (one 16-byte load) times 16 fp32 activations, biased form.
+__device__ __forceinline__ float dot16_biased(const u32x4 wq, const float* xf, float acc) {
+  const uint32_t d[4] = {wq.x ^ 0x80808080u, wq.y ^ 0x80808080u, wq.z ^ 0x80808080u, wq.w ^ 0x80808080u};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc = fmaf((float)(d[j] & 0xffu), xf[4 * j + 0], acc);
+    acc = fmaf((float)((d[j] >> 8) & 0xffu), xf[4 * j + 1], acc);
+    acc = fmaf((float)((d[j] >> 16) & 0xffu), xf[4 * j + 2], acc);
+    acc = fmaf((float)(d[j] >> 24), xf[4 * j + 3], acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void unpack_bf16x16(const u32x4 a, const u32x4 b, float* xf) {
+  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xf[2 * i] = bf16_lo(u[i]);
+    xf[2 * i + 1] = bf16_hi(u[i]);
+  }
+}
+
+// Fast path. Preconditions (checked on the host): every K chunk boundary and
+// every row start is 16-byte aligned (K % 16 == 0, kchunk % 16 == 0, ldw % 16 == 0,
+// ldx % 8 == 0, aligned base pointers). NCH > 0 means each split covers exactly
+// NCH * kChunk elements, so the chunk loop is fully unrolled with no K masking.
+// Rows past N and x rows past m_rows are clamped to valid memory and discarded.
+template <int M, int R, int NCH, int EPI>
+__global__ __launch_bounds__(kGemvThreads) void gemv_i8_rows(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, void* __restrict__ out, int64_t ldo, int m_rows, int N, int K,
+    int kchunk) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t row0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * R;
+  if (row0 >= N) return;
+  const int k_begin = blockIdx.y * kchunk;
+  const int k_end = min(K, k_begin + kchunk);
+
+  const int8_t* wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wrow[r] = w + min(row0 + r, (int64_t)N - 1) * ldw;
+  const uint16_t* xrow[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xrow[m] = x + (int64_t)min(m, m_rows - 1) * ldx;
+
+  float acc[M][R];
+  float sx[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    sx[m] = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+  }
+
+  const int nch = NCH > 0 ? NCH : (k_end - k_begin + kChunk - 1) / kChunk;
+#pragma unroll
+  for (int c = 0; c < nch; ++c) {
+    const int k = k_begin + c * kChunk + lane * 16;
+    if (NCH > 0 || k < k_end) {
+      u32x4 wv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[r] = ld16_stream(wrow[r] + k);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float xf[16];
+        unpack_bf16x16(ld16(xrow[m] + k), ld16(xrow[m] + k + 8), xf);
+        float t = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t += xf[e];
+        sx[m] += t;
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = dot16_biased(wv[r], xf, acc[m][r]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float mine = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[m][r] - 128.f * sx[m]);
+      if (lane == r) mine = v;
+    }
+    const int64_t n = row0 + lane;
+    if (lane < R && m < m_rows && n < N) {
+      if constexpr (EPI == kEpiStore) {
+        ((uint16_t*)out)[(int64_t)m * ldo + n] = f32_to_bf16(mine * scale[n]);
+      } else {
+        ((float*)out)[((int64_t)blockIdx.y * m_rows + m) * ldo + n] = mine;
+      }
+    }
+  }
+}
+
+// Any alignment, any K: one wavefront per output row, one element per lane step.
+// Used for shapes the fast path does not take (odd K, unaligned rows).
+__global__ __launch_bounds__(kGemvThreads) void gemv_i8_generic(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, void* __restrict__ out, int64_t ldo, int m_rows, int N, int K,
+    int kchunk, int epi) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t n = (int64_t)blockIdx.x * kGemvWaves + wave;
+  if (n >= N) return;
+  const int k_begin = blockIdx.y * kchunk;
+  const int k_end = min(K, k_begin + kchunk);
+  const int8_t* wr = w + n * ldw;
+  for (int m = 0; m < m_rows; ++m) {
+    const uint16_t* xr = x + (int64_t)m * ldx;
+    float a = 0.f;
+    for (int k = k_begin + lane; k < k_end; k += kWave) a = fmaf(bf16_to_f32(xr[k]), (float)wr[k], a);
+    a = wave_sum(a);
+    if (lane == 0) {
+      if (epi == kEpiStore) {
+        ((uint16_t*)out)[(int64_t)m * ldo + n] = f32_to_bf16(a * scale[n]);
+      } else {
+        ((float*)out)[((int64_t)blockIdx.y * m_rows + m) * ldo + n] = a;
+      }
+    }
+  }
+}
+
+// Deterministic split-K reduction: fixed split order, then scale, one rounding.
+__global__ __launch_bounds__(256) void gemv_splitk_reduce(const float* __restrict__ part, int splits, int m_rows,
+                                                          int N, const float* __restrict__ scale,
+                                                          uint16_t* __restrict__ y, int64_t ldy) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (n >= N) return;
+  float a = 0.f;
+  for (int s = 0; s < splits; ++s) a += part[((int64_t)s * m_rows + m) * N + n];
+  y[(int64_t)m * ldy + n] = f32_to_bf16(a * scale[n]);
+}
+
+struct GemvArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const int8_t* w;
+  int64_t ldw;
+  const float* scale;
+  void* out;
+  int64_t ldo;
+  int m_rows, N, K, kchunk, splits;
+};
+
+template <int M, int R, int NCH, int EPI>
+void launch_rows(const GemvArgs& a, hipStream_t st) {
+  const int rows_per_block = kGemvWaves * R;
+  dim3 grid((unsigned)((a.N + rows_per_block - 1) / rows_per_block), (unsigned)a.splits);
+  hipLaunchKernelGGL((gemv_i8_rows<M, R, NCH, EPI>), grid, dim3(kGemvThreads), 0, st, a.x, a.ldx, a.w, a.ldw,
+                     a.scale, a.out, a.ldo, a.m_rows, a.N, a.K, a.kchunk);
+}
+
+// Rows per wavefront: enough blocks to cover the 256 CUs at least twice, capped
+// by register budget (R * chunks of 16-byte loads in flight per lane).
+int pick_rows(int N, int m_tile) {
+  const int cap = m_tile == 1 ? 4 : (m_tile <= 4 ? 2 : 1);
+  int r = 1;
+  while (r < cap && (int64_t)N >= (int64_t)(2 * r) * kGemvWaves * 512) r *= 2;
+  return r;
+}
+
+template <int M, int EPI>
+void launch_fast_m(const GemvArgs& a, int nch_exact, hipStream_t st) {
+  const int r = pick_rows(a.N, M);
+  if constexpr (M == 1) {
+    // Fully unrolled chunk loops for the common per-split lengths.
+#define EGPT_NCH_CASE(NC)                                              \
+  if (nch_exact == NC) {                                               \
+    if (r == 4) return launch_rows<1, 4, NC, EPI>(a, st);              \
+    if (r == 2) return launch_rows<1, 2, NC, EPI>(a, st);              \
+    return launch_rows<1, 1, NC, EPI>(a, st);                          \
+  }
+    EGPT_NCH_CASE(1)
+    EGPT_NCH_CASE(2)
+    EGPT_NCH_CASE(3)
+    EGPT_NCH_CASE(4)
+    EGPT_NCH_CASE(6)
+#undef EGPT_NCH_CASE
+    if (r == 4) return launch_rows<1, 4, 0, EPI>(a, st);
+    if (r == 2) return launch_rows<1, 2, 0, EPI>(a, st);
+    return launch_rows<1, 1, 0, EPI>(a, st);
+  } else {
+    if (r >= 2) return launch_rows<M, 2, 0, EPI>(a, st);
+    return launch_rows<M, 1, 0, EPI>(a, st);
+  }
+}
+
+template <int EPI>
+int launch_gemv(const GemvArgs& a, hipStream_t st) {
+  const bool aligned = (a.K % 16 == 0) && (a.kchunk % 16 == 0) && (a.ldw % 16 == 0) &&
+                       ((uintptr_t)a.w % 16 == 0) && ((uintptr_t)a.x % 16 == 0) &&
+                       (a.m_rows == 1 || a.ldx % 8 == 0);
+  if (!aligned || a.K == 0) {
+    dim3 grid((unsigned)((a.N + kGemvWaves - 1) / kGemvWaves), (unsigned)a.splits);
+    hipLaunchKernelGGL(gemv_i8_generic, grid, dim3(kGemvThreads), 0, st, a.x, a.ldx, a.w, a.ldw, a.scale, a.out,
+                       a.ldo, a.m_rows, a.N, a.K, a.kchunk, EPI);
+    return EGPT_LAUNCH_STATUS();
+  }
+  // Exact chunk count per split when every split has the same length.
+  int nch_exact = 0;
+  if (a.kchunk % kChunk == 0 && (int64_t)a.kchunk * a.splits == a.K) nch_exact = a.kchunk / kChunk;
+  const int mt = a.m_rows;
+  if (mt == 1) launch_fast_m<1, EPI>(a, nch_exact, st);
+  else if (mt <= 2) launch_fast_m<2, EPI>(a, nch_exact, st);
+  else if (mt <= 4) launch_fast_m<4, EPI>(a, nch_exact, st);
+  else if (mt <= 8) launch_fast_m<8, EPI>(a, nch_exact, st);
+  else launch_fast_m<16, EPI>(a, nch_exact, st);
+  return EGPT_LAUNCH_STATUS();
+}
+
+int check_gemv_args(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, const void* y,
+                    int64_t ldy, int M, int N, int K) {
+  if (!x || !w || !scale || !y) return EGPT_ERR_INVALID;
+  if (M < 0 || N < 0 || K < 0) return EGPT_ERR_INVALID;
+  if (M > EGPT_MAX_DECODE_ROWS) return EGPT_ERR_UNSUPPORTED;
+  if (ldw < K || (M > 1 && (ldx < K || ldy < N))) return EGPT_ERR_INVALID;
+  return EGPT_OK;
+}
+
+}  // namespace
+}  // namespace egpt
+
+using namespace egpt;
+
+extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale,
+                              void* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+  const int st = check_gemv_args(x, ldx, w, ldw, scale, y, ldy, M, N, K);
+  if (st != EGPT_OK) return st;
+  if (M == 0 || N == 0) return EGPT_OK;
+  GemvArgs a{(const uint16_t*)x, ldx, w, ldw, scale, y, ldy, M, N, K, K > 0 ? K : 1, 1};
+  return launch_gemv<kEpiStore>(a, stream);
+}
+
+extern "C" int egpt_int8_gemv_splitk_workspace(int M, int N, int K, int splits, size_t* bytes) {
+  if (!bytes || M < 0 || N < 0 || K < 0 || splits < 1) return EGPT_ERR_INVALID;
+  *bytes = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
+  return EGPT_OK;
+}
+
+extern "C" int egpt_int8_gemv_splitk(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale,
+                                     void* y, int64_t ldy, int M, int N, int K, int splits, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+  int st = check_gemv_args(x, ldx, w, ldw, scale, y, ldy, M, N, K);
+  if (st != EGPT_OK) return st;
+  if (splits < 1) return EGPT_ERR_INVALID;
+  if (M == 0 || N == 0) return EGPT_OK;
+  // K chunk per split: a multiple of 16 so the aligned fast path stays available;
+  // the number of splits actually launched may shrink so no split is empty.
+  int kchunk = (K + splits - 1) / splits;
+  kchunk = ((kchunk + 15) / 16) * 16;
+  if (kchunk == 0) kchunk = 16;
+  const int used = (K + kchunk - 1) / kchunk > 0 ? (K + kchunk - 1) / kchunk : 1;
+  size_t need = 0;
+  egpt_int8_gemv_splitk_workspace(M, N, K, used, &need);
+  if (!workspace || workspace_bytes < need) return EGPT_ERR_WORKSPACE;
+  GemvArgs a{(const uint16_t*)x, ldx, w, ldw, scale, workspace, N, M, N, K, kchunk, used};
+  st = launch_gemv<kEpiPartial>(a, stream);
+  if (st != EGPT_OK) return st;
+  dim3 grid((unsigned)((N + 255) / 256), (unsigned)M);
+  hipLaunchKernelGGL(gemv_splitk_reduce, grid, dim3(256), 0, stream, (const float*)workspace, used, M, N, scale,
+                     (uint16_t*)y, M > 1 ? ldy : (int64_t)N);
+  return EGPT_LAUNCH_STATUS();
+}

@@ -1,0 +1,57 @@
+"""The C ABI library loads and exports exactly what include/egpt.h declares (CPU: no kernel launches)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from efficientgpt_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / 'include' / 'egpt.h'
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(egpt_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.egpt_abi_version() == _lib.ABI_VERSION
+    assert lib.egpt_status_string(0) == b'ok'
+
+
+def test_argument_errors_return_status_without_launching():
+    lib = _lib.lib()
+    dummy = ctypes.c_void_p(16)
+    # null operands
+    assert lib.egpt_int8_gemv(None, 0, dummy, 16, dummy, dummy, 0, 1, 16, 16, None) == -1
+    # more rows than the decode kernel takes
+    assert lib.egpt_int8_gemv(dummy, 16, dummy, 16, dummy, dummy, 16, 17, 16, 16, None) == -2
+    # row stride shorter than K
+    assert lib.egpt_int8_gemv(dummy, 16, dummy, 8, dummy, dummy, 16, 1, 16, 16, None) == -1
+    size = ctypes.c_size_t()
+    assert lib.egpt_int8_gemv_splitk_workspace(2, 100, 64, 4, ctypes.byref(size)) == 0
+    assert size.value == 4 * 2 * 100 * 4
+    assert lib.egpt_int8_gemv_splitk(dummy, 64, dummy, 64, dummy, dummy, 100, 2, 100, 64, 4, None, 0, None) == -4
+    # attention: Hq not a multiple of Hkv, unsupported dtype, missing workspace
+    args = [dummy, 0, 0, dummy, 0, 0, 0, dummy, 0, 0, 0, dummy, 0, dummy, 0, 0]
+    assert lib.egpt_decode_attn(1, *args, None, 0, 1, 6, 4, 64, 128, 1, 0.1, None) == -1
+    assert lib.egpt_decode_attn(7, *args, None, 0, 1, 8, 4, 64, 128, 1, 0.1, None) == -2
+    assert lib.egpt_decode_attn(1, *args, None, 0, 1, 8, 4, 64, 128, 1, 0.1, None) == -4
+    assert lib.egpt_decode_attn_workspace(1, 16, 8, 4096, 128, 8, ctypes.byref(size)) == 0
+    assert size.value >= 16 * 8 * (128 + 2) * 4
+
+
+@pytest.mark.parametrize('b,hkv,cap', [(1, 8, 256), (1, 8, 32768), (16, 6, 128), (1, 1, 1)])
+def test_default_splits_bounded(b, hkv, cap):
+    n = _lib.lib().egpt_decode_attn_default_splits(b, hkv, cap)
+    assert 1 <= n <= 256 and n <= max(1, cap)

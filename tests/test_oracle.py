@@ -1,0 +1,234 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP kernels."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import int8 as oint8
+from oracle.numerics import bf16_bits, from_bf16_bits, to_bf16
+
+
+# ---------------------------------------------------------------- bf16 rounding
+
+def test_bf16_known_bits_and_ties_to_even():
+    # 1 + 2^-8 is exactly half-way between bf16 1.0 and 1.0078125: ties to even -> 1.0
+    # 1 + 3 * 2^-8 is half-way between 1.0078125 (odd) and 1.015625 (even) -> 1.015625
+    vals = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 3.4e38, np.inf, -0.0], np.float32)
+    got = to_bf16(vals)
+    assert got[0] == 1.0 and got[1] == 1.0 and got[2] == 1.015625 and got[3] == -2.5
+    assert np.isinf(got[4]) and np.isinf(got[5]) and np.signbit(got[6])
+    assert np.isnan(to_bf16(np.array([np.nan], np.float32)))[0]
+    assert bf16_bits(np.array([1.0], np.float32))[0] == 0x3F80
+    assert from_bf16_bits(np.array([0xC020], np.uint16))[0] == -2.5
+
+
+def test_bf16_matches_torch_cast():
+    x = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 1e3
+    ours = to_bf16(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours, theirs)
+
+
+# ---------------------------------------------------------------- int8 quantisation
+
+def test_quantize_known_answer_half_even():
+    # max |w| = 1 -> s = 1/127; -0.5 / s = -63.5 rounds to the even -64; 0.25 / s = 31.75 -> 32
+    q, s = oint8.quantize_weight(np.array([[1.0, -0.5, 0.25], [0.0, 0.0, 0.0]], np.float32))
+    assert s[0] == np.float32(1.0) / np.float32(127.0)
+    assert q[0].tolist() == [127, -64, 32]
+    assert s[1] == np.float32(1e-12) and q[1].tolist() == [0, 0, 0]
+
+
+def test_quantize_invariants_and_torch_agreement():
+    # research/realmodel/test_int8_linear.py:43-53: closed form, |q|max = 127, half-step reconstruction
+    rng = np.random.default_rng(1)
+    w = rng.standard_normal((300, 128)).astype(np.float32)
+    q, s = oint8.quantize_weight(w)
+    assert q.dtype == np.int8 and int(np.abs(q.astype(np.int32)).max(axis=1).min()) == 127
+    assert float(np.abs(q.astype(np.float32) * s[:, None] - w).max()) <= float(s.max()) / 2 + 1e-6
+    from efficientgpt_amd.int8_linear import quantize_weight as product_quantize
+    tq, ts = product_quantize(torch.from_numpy(w))
+    assert np.array_equal(tq.numpy(), q) and np.array_equal(ts.numpy(), s)
+
+
+def test_quantize_row_blocks_match_whole_matrix():
+    from efficientgpt_amd.int8_linear import quantize_weight as product_quantize
+    big = torch.randn(20000, 64, generator=torch.Generator().manual_seed(2))  # > one 8192-row block
+    qb, sb = product_quantize(big)
+    s_ref = (big.abs().amax(1) / 127.0).clamp_min(1e-12)
+    assert torch.equal(sb, s_ref)
+    assert torch.equal(qb, torch.round(big / s_ref[:, None]).clamp(-127, 127).to(torch.int8))
+
+
+# ---------------------------------------------------------------- int8 linear formulas
+
+def _int8_case(m, k, n, seed=0):
+    rng = np.random.default_rng(seed)
+    x = to_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s = (rng.random(n).astype(np.float32) * 0.02 + 1e-3).astype(np.float32)
+    return x, q, s
+
+
+def test_linear_decode_equals_brute_force_loops():
+    x, q, s = _int8_case(3, 100, 70)
+    want = np.zeros((3, 70), np.float64)
+    for i in range(3):
+        for j in range(70):
+            acc = 0.0
+            for kk in range(100):
+                acc += float(x[i, kk]) * float(q[j, kk])
+            want[i, j] = acc
+    got = oint8.linear_decode(x, q, s)
+    ref = to_bf16((want.astype(np.float32) * s[None, :]).astype(np.float32))
+    assert np.array_equal(got, ref)
+
+
+def test_linear_formulas_within_reference_tolerance():
+    for m, k, n in [(1, 2048, 256), (4, 512, 64), (16, 256, 48), (17, 256, 32)]:
+        x, q, s = _int8_case(m, k, n, seed=m)
+        tol = oint8.tolerance_vs_naive(x, q, s)
+        assert oint8.max_err(oint8.linear_decode(x, q, s), x, q, s) <= tol
+        assert oint8.max_err(oint8.linear_prefill(x, q, s), x, q, s) <= tol
+        assert oint8.max_err(oint8.linear(x, q, s), x, q, s) <= oint8.tolerance_vs_eager(x, q, s)
+
+
+def test_tolerance_rejects_planted_mistakes():
+    # the mutations research/kernelagent/test_evaluate.py:86-95 must reject
+    x, q, s = _int8_case(1, 2048, 512, seed=3)
+    tol = oint8.tolerance_vs_eager(x, q, s)
+    no_scale = to_bf16((x.astype(np.float64) @ q.astype(np.float64).T).astype(np.float32))
+    assert oint8.max_err(no_scale, x, q, s) > tol
+    skip_last = oint8.linear_decode(x[:, :-128], q[:, :-128], s)
+    assert oint8.max_err(skip_last, x, q, s) > tol
+    unsigned = oint8.linear_decode(x, q.view(np.uint8).astype(np.float32), s)
+    assert oint8.max_err(unsigned, x, q, s) > tol
+
+
+def test_linear_row_rule():
+    x, q, s = _int8_case(17, 64, 32, seed=4)
+    assert np.array_equal(oint8.linear(x, q, s), oint8.linear_prefill(x, q, s))
+    assert np.array_equal(oint8.linear(x[:16], q, s), oint8.linear_decode(x[:16], q, s))
+
+
+# ---------------------------------------------------------------- attention
+
+def _attn_case(b, hq, hkv, cap, d, seed=0, scale=1.0):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((b, hq, 1, d)) * scale
+    k = rng.standard_normal((b, hkv, cap, d)) * scale
+    v = rng.standard_normal((b, hkv, cap, d))
+    return q, k, v
+
+
+def test_attention_position_zero_returns_first_value():
+    q, k, v = _attn_case(2, 4, 2, 9, 64)
+    out = oatt.attention_truth(q, k, v, np.array([0, 0]))
+    assert np.allclose(out[:, :, 0], np.repeat(v[:, :, 0], 2, axis=1), rtol=0, atol=1e-15)
+
+
+def test_attention_constant_keys_give_mean_of_values():
+    q, k, v = _attn_case(1, 4, 4, 20, 64)
+    k[:] = 0.3
+    out = oatt.attention_truth(q, k, v, np.array([12]))
+    assert np.allclose(out[0, :, 0], v[0, :, :13].mean(axis=1), atol=1e-12)
+
+
+def test_attention_gqa_equals_repeated_mha_and_torch_sdpa():
+    q, k, v = _attn_case(3, 8, 2, 37, 64, seed=5, scale=2.0)
+    pos = np.array([3, 36, 20])
+    gqa = oatt.attention_truth(q, k, v, pos)
+    mha = oatt.attention_truth(q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), pos)
+    assert np.array_equal(gqa, mha)
+    tq, tk, tv = (torch.from_numpy(a) for a in (q, np.repeat(k, 4, 1), np.repeat(v, 4, 1)))
+    allowed = torch.arange(37).view(1, 1, 1, 37) <= torch.from_numpy(pos).view(-1, 1, 1, 1)
+    sdpa = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=allowed).numpy()
+    assert np.allclose(gqa, sdpa, atol=1e-12, rtol=0)
+
+
+def test_attention_splitk_restatement_tracks_truth_and_ignores_poison():
+    q, k, v = _attn_case(2, 4, 2, 80, 64, seed=6, scale=8.0)
+    pos = np.array([0, 61])
+    truth = oatt.attention_truth(q, k, v, pos)
+    for split, block in ((16, 16), (64, 32), (80, 80)):
+        got = oatt.attention_splitk(q, k, v, pos, split=split, block_n=block)
+        assert np.abs(got - truth).max() < 1e-5
+    poisoned_k, poisoned_v = k.copy(), v.copy()
+    for b, p in enumerate(pos):
+        poisoned_k[b, :, p + 1:] = np.nan
+        poisoned_v[b, :, p + 1:] = np.nan
+    assert np.array_equal(oatt.attention_splitk(q, poisoned_k, poisoned_v, pos), oatt.attention_splitk(q, k, v, pos))
+
+
+def test_attention_mask_off_by_one_is_caught():
+    # reading one slot past the position (research/kernelagent/test_evaluate.py:45-48) must exceed the tolerance
+    q, k, v = _attn_case(1, 4, 2, 64, 64, seed=7)
+    pos = np.array([30])
+    truth = oatt.attention_truth(q, k, v, pos)
+    wrong = oatt.attention_truth(q, k, v, pos + 1)
+    assert np.abs(wrong - truth).max() > 1e-3
+
+
+# ---------------------------------------------------------------- Qwen3 step vs transformers
+
+def _fp32_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """transformers attention hook with the decode kernel's contract: fp32 math, causal over the cache."""
+    g = query.shape[1] // key.shape[1]
+    k = key.float().repeat_interleave(g, 1)
+    v = value.float().repeat_interleave(g, 1)
+    s = (query.float() @ k.transpose(-1, -2)) * scaling
+    t, n = s.shape[-2], s.shape[-1]
+    allowed = torch.arange(n)[None, :] <= (n - t + torch.arange(t))[:, None]
+    s = s.masked_fill(~allowed, float('-inf'))
+    return (torch.softmax(s, -1) @ v).to(query.dtype).transpose(1, 2).contiguous(), None
+
+
+@pytest.fixture(scope='module')
+def tiny_hf():
+    transformers = pytest.importorskip('transformers')
+    transformers.AttentionInterface.register('egpt_fp32_test', _fp32_attention)
+    cfg = transformers.Qwen3Config(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                                   max_position_embeddings=256, tie_word_embeddings=True, initializer_range=0.2,
+                                   attn_implementation='egpt_fp32_test')
+    return transformers, cfg
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_qwen3_oracle_matches_transformers(tiny_hf, dtype):
+    from oracle.qwen3 import TINY, Qwen3Oracle
+    transformers, cfg = tiny_hf
+    torch.manual_seed(0)
+    model = transformers.Qwen3ForCausalLM(cfg).to(dtype).eval()
+    with torch.no_grad():  # jitter the norm weights so a swapped q/k norm shows
+        for name, p in model.named_parameters():
+            if 'norm' in name:
+                p.add_((0.1 * torch.randn(p.shape)).to(dtype))
+    orc = Qwen3Oracle(TINY, model.state_dict(), dtype=dtype, cap=128, inv_freq=model.model.rotary_emb.inv_freq)
+    g = torch.Generator().manual_seed(1)
+    for p in (1, 5, 37):
+        x = torch.randint(0, 512, (1, p), generator=g)
+        with torch.no_grad():
+            want = model.generate(input_ids=x, attention_mask=torch.ones_like(x), max_new_tokens=24,
+                                  min_new_tokens=24, do_sample=False, pad_token_id=0)[0, p:].tolist()
+            hf_logits = model(x, logits_to_keep=1).logits[0, -1].float()
+        got = orc.greedy(x[0], 24)
+        assert len(set(got)) > 8
+        assert got == want, (dtype, p)
+        orc.reset()
+        diff = float((orc.forward(x[0], 0).float() - hf_logits).abs().max())
+        assert diff <= (0.0 if dtype == torch.bfloat16 else 1e-4), diff
+
+
+def test_qwen3_oracle_int8_rule_uses_decode_and_prefill_formulas():
+    from oracle.qwen3 import Linear
+    g = torch.Generator().manual_seed(3)
+    q = torch.randint(-127, 128, (48, 64), generator=g, dtype=torch.int8)
+    s = torch.rand(48, generator=g) * 0.01 + 1e-3
+    lin = Linear(qweight=q, scale=s)
+    for rows in (1, 16, 17, 40):
+        x = torch.randn(rows, 64, generator=g).to(torch.bfloat16)
+        got = lin(x).float().numpy()
+        want = oint8.linear(x.float().numpy(), q.numpy(), s.numpy())
+        assert np.array_equal(got, want), rows
