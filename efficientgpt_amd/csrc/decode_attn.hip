@@ -279,6 +279,7 @@ template <typename T>
 int dispatch_dim(const AttnArgs& a, int D, hipStream_t st) {
   if (D == 128) return dispatch_group<T, 128>(a, st);
   if (D == 64) return dispatch_group<T, 64>(a, st);
+  if (D == 32) return dispatch_group<T, 32>(a, st);
   return EGPT_ERR_UNSUPPORTED;
 }
 

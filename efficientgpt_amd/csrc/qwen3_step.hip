@@ -1,0 +1,324 @@
+// Elementwise / normalisation kernels of the Qwen3 decode step on gfx950.
+//
+// Rounding follows transformers' bf16 Qwen3 (models/qwen3/modeling_qwen3.py), op by op:
+//   RMSNorm      y = bf16( w * bf16( x * rsqrt(mean(x^2) + eps) ) ), statistics in fp32  (:30-46)
+//   residual     x = bf16( x + a )                                                      (:285-322)
+//   q/k norm     RMSNorm over head_dim on each head                                      (:237-238, :255-256)
+//   RoPE         bf16( bf16(x * cos) + bf16(rotate_half(x) * sin) ), cos/sin tables bf16 (:139-166)
+//   SwiGLU       bf16( bf16(silu(gate)) * up )                                           (:49-62)
+//   argmax       first index of the largest logit (torch.argmax), next token + position
+//                advance of the reference's graph step (research/realmodel/fast_decode.py:45-49)
+// All activations are bf16 stored as uint16.
+#include "common.h"
+
+namespace egpt {
+namespace {
+
+constexpr int kNormThreads = 256;
+
+__device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Block-wide sum with a fixed order: wave sums, then the four wave totals in order.
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return total;
+}
+
+// One block per row. If `a` is non-null the residual is updated first:
+// x = bf16(x + a) (written back), then y = RMSNorm(x).
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(uint16_t* __restrict__ x, int64_t ldx,
+                                                                   const uint16_t* __restrict__ a, int64_t lda,
+                                                                   const uint16_t* __restrict__ w,
+                                                                   uint16_t* __restrict__ y, int64_t ldy, int n,
+                                                                   float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  extern __shared__ float rowbuf[];  // n floats: the (updated) residual row
+  const int64_t row = blockIdx.x;
+  uint16_t* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += kNormThreads) {
+    float v = bf16_to_f32(xr[i]);
+    if (a) {
+      v = bf16r(v + bf16_to_f32(a[row * lda + i]));
+      xr[i] = f32_to_bf16(v);
+    }
+    rowbuf[i] = v;
+    ss = fmaf(v, v, ss);
+  }
+  const float total = block_sum_256(ss, red);
+  const float inv = rsqrtf(total / (float)n + eps);
+  uint16_t* yr = y + row * ldy;
+  for (int i = threadIdx.x; i < n; i += kNormThreads) {
+    yr[i] = f32_to_bf16(bf16_to_f32(w[i]) * bf16r(rowbuf[i] * inv));
+  }
+}
+
+// q/k RMSNorm + RoPE + cache write. One wavefront per (row, head); heads
+// 0..Hq-1 are query heads (written to q_out), Hq..Hq+Hkv-1 key heads (normed,
+// rotated, written to the key cache at the row's position), the last Hkv value
+// heads (copied to the value cache). Row layout of qkv: [q(Hq*D) | k(Hkv*D) | v(Hkv*D)].
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld_qkv, const int64_t* __restrict__ positions,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, uint16_t* __restrict__ q_out, int64_t ld_q, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int64_t c_sh, int64_t c_sn, int rows, int Hq, int Hkv, int cap, float eps) {
+  constexpr int EPT = D >= kWave ? D / kWave : 1;  // elements per lane (2 for D = 128)
+  static_assert(D % kWave == 0 || kWave % D == 0, "head_dim must divide or be a multiple of 64");
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool live = lane < D;  // D < 64: the upper lanes hold no element
+  const int64_t job = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int heads = Hq + 2 * Hkv;
+  if (job >= (int64_t)rows * heads) return;
+  const int64_t row = job / heads;
+  const int head = (int)(job % heads);
+  int64_t pos = positions[row];
+  pos = pos < 0 ? 0 : (pos >= cap ? cap - 1 : pos);
+  const uint16_t* src = qkv + row * ld_qkv + (int64_t)head * D;
+  if (head >= Hq + Hkv) {  // value head: straight copy into the cache
+    uint16_t* dst = v_cache + (int64_t)(head - Hq - Hkv) * c_sh + pos * c_sn;
+    if (live) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) dst[lane + e * kWave] = src[lane + e * kWave];
+    }
+    return;
+  }
+  const bool is_q = head < Hq;
+  const uint16_t* nw = is_q ? qn_w : kn_w;
+  float xv[EPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    xv[e] = live ? bf16_to_f32(src[lane + e * kWave]) : 0.f;
+    ss = fmaf(xv[e], xv[e], ss);
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+  // Normed values. Lane l holds elements l + 64 e; rotate_half pairs element i
+  // with i +- D/2, which for D = 128 sits in the same lane (e +- 1) and for
+  // D = 64 in lane l ^ 32 (same e).
+  float nv[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) nv[e] = live ? bf16r(bf16_to_f32(nw[lane + e * kWave]) * bf16r(xv[e] * inv)) : 0.f;
+  const uint16_t* cr = cos_t + pos * D;
+  const uint16_t* sr = sin_t + pos * D;
+  uint16_t out[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = lane + e * kWave;
+    float partner;
+    if constexpr (D / 2 >= kWave) {
+      constexpr int kHalf = D / 2 / kWave;
+      partner = e < kHalf ? nv[(e + kHalf) % EPT] : nv[(e + EPT - kHalf) % EPT];
+    } else {
+      partner = __shfl_xor(nv[e], D / 2, kWave);
+    }
+    const float rh = i % D < D / 2 ? -partner : partner;
+    out[e] = live ? f32_to_bf16(bf16r(nv[e] * bf16_to_f32(cr[i])) + bf16r(rh * bf16_to_f32(sr[i]))) : 0;
+  }
+  uint16_t* dst = is_q ? q_out + row * ld_q + (int64_t)head * D
+                       : k_cache + (int64_t)(head - Hq) * c_sh + pos * c_sn;
+  if (live) {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) dst[lane + e * kWave] = out[e];
+  }
+}
+
+// act = bf16( bf16(silu(gate)) * up ), gate/up interleaved per row as [gate(inter) | up(inter)].
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t ld_gu, int inter,
+                                                       uint16_t* __restrict__ out, int64_t ld_out, int rows) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)rows * inter) return;
+  const int64_t row = i / inter;
+  const int c = (int)(i % inter);
+  const float g = bf16_to_f32(gu[row * ld_gu + c]);
+  const float u = bf16_to_f32(gu[row * ld_gu + inter + c]);
+  const float sg = bf16r(g / (1.0f + expf(-g)));
+  out[row * ld_out + c] = f32_to_bf16(sg * u);
+}
+
+// Embedding gather: out[r, :] = table[token[r], :].
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ tokens, const uint16_t* __restrict__ table,
+                                                    int64_t ld_table, int vocab, uint16_t* __restrict__ out,
+                                                    int64_t ld_out, int n) {
+  const int64_t row = blockIdx.y;
+  int64_t t = tokens[row];
+  t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    out[row * ld_out + i] = table[t * ld_table + i];
+}
+
+// argmax, stage 1: each block reduces a contiguous range to (max, first index).
+// A logit compares larger if greater, or equal with a smaller index.
+struct ArgBest {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+__device__ __forceinline__ ArgBest wave_arg(ArgBest x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    ArgBest o;
+    o.v = __shfl_xor(x.v, off, kWave);
+    o.i = __shfl_xor(x.i, off, kWave);
+    x = arg_better(x, o);
+  }
+  return x;
+}
+
+constexpr int kArgThreads = 256;
+
+__device__ ArgBest block_arg(ArgBest x) {
+  __shared__ float sv[kArgThreads / kWave];
+  __shared__ int si[kArgThreads / kWave];
+  x = wave_arg(x);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[wave] = x.v;
+    si[wave] = x.i;
+  }
+  __syncthreads();
+  ArgBest r{sv[0], si[0]};
+#pragma unroll
+  for (int j = 1; j < kArgThreads / kWave; ++j) r = arg_better(r, ArgBest{sv[j], si[j]});
+  return r;
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(const uint16_t* __restrict__ logits, int n,
+                                                                     int per_block, float* __restrict__ pv,
+                                                                     int* __restrict__ pi) {
+  const int begin = blockIdx.x * per_block;
+  const int end = min(n, begin + per_block);
+  ArgBest best{-INFINITY, 0x7fffffff};
+  for (int i = begin + threadIdx.x; i < end; i += kArgThreads) best = arg_better(best, ArgBest{bf16_to_f32(logits[i]), i});
+  best = block_arg(best);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = best.v;
+    pi[blockIdx.x] = best.i;
+  }
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_final_kernel(const float* __restrict__ pv,
+                                                                   const int* __restrict__ pi, int parts,
+                                                                   int64_t* __restrict__ token,
+                                                                   int64_t* __restrict__ position) {
+  ArgBest best{-INFINITY, 0x7fffffff};
+  for (int j = threadIdx.x; j < parts; j += kArgThreads) best = arg_better(best, ArgBest{pv[j], pi[j]});
+  best = block_arg(best);
+  if (threadIdx.x == 0) {
+    *token = best.i == 0x7fffffff ? 0 : best.i;  // all-NaN logits: token 0
+    if (position) *position += 1;
+  }
+}
+
+constexpr int kArgParts = 256;
+
+}  // namespace
+}  // namespace egpt
+
+using namespace egpt;
+
+extern "C" int egpt_rmsnorm(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int rows, int n, float eps,
+                            hipStream_t stream) {
+  if (!x || !w || !y || rows < 0 || n < 1 || ldx < n || ldy < n) return EGPT_ERR_INVALID;
+  if ((size_t)n * sizeof(float) > 64 * 1024) return EGPT_ERR_UNSUPPORTED;
+  if (rows == 0) return EGPT_OK;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), n * sizeof(float), stream, (uint16_t*)x, ldx,
+                     (const uint16_t*)nullptr, 0, (const uint16_t*)w, (uint16_t*)y, ldy, n, eps);
+  return EGPT_LAUNCH_STATUS();
+}
+
+extern "C" int egpt_add_rmsnorm(void* x, int64_t ldx, const void* a, int64_t lda, const void* w, void* y, int64_t ldy,
+                                int rows, int n, float eps, hipStream_t stream) {
+  if (!x || !a || !w || !y || rows < 0 || n < 1 || ldx < n || lda < n || ldy < n) return EGPT_ERR_INVALID;
+  if ((size_t)n * sizeof(float) > 64 * 1024) return EGPT_ERR_UNSUPPORTED;
+  if (rows == 0) return EGPT_OK;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), n * sizeof(float), stream, (uint16_t*)x, ldx,
+                     (const uint16_t*)a, lda, (const uint16_t*)w, (uint16_t*)y, ldy, n, eps);
+  return EGPT_LAUNCH_STATUS();
+}
+
+extern "C" int egpt_qk_norm_rope(const void* qkv, int64_t ld_qkv, const int64_t* positions, const void* q_norm_w,
+                                 const void* k_norm_w, const void* cos_t, const void* sin_t, void* q_out, int64_t ld_q,
+                                 void* k_cache, void* v_cache, int64_t cache_head_stride, int64_t cache_slot_stride,
+                                 int rows, int Hq, int Hkv, int D, int cap, float eps, hipStream_t stream) {
+  if (!qkv || !positions || !q_norm_w || !k_norm_w || !cos_t || !sin_t || !q_out || !k_cache || !v_cache)
+    return EGPT_ERR_INVALID;
+  if (rows < 0 || Hq < 1 || Hkv < 1 || cap < 1 || ld_qkv < (int64_t)(Hq + 2 * Hkv) * D || ld_q < (int64_t)Hq * D)
+    return EGPT_ERR_INVALID;
+  if (rows == 0) return EGPT_OK;
+  const int64_t jobs = (int64_t)rows * (Hq + 2 * Hkv);
+  dim3 grid((unsigned)((jobs + 3) / 4));
+  if (D == 128) {
+    hipLaunchKernelGGL((qk_norm_rope_kernel<128>), grid, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, positions,
+                       (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,
+                       (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                       cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps);
+  } else if (D == 64) {
+    hipLaunchKernelGGL((qk_norm_rope_kernel<64>), grid, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, positions,
+                       (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,
+                       (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                       cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps);
+  } else if (D == 32) {
+    hipLaunchKernelGGL((qk_norm_rope_kernel<32>), grid, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, positions,
+                       (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,
+                       (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                       cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps);
+  } else {
+    return EGPT_ERR_UNSUPPORTED;
+  }
+  return EGPT_LAUNCH_STATUS();
+}
+
+extern "C" int egpt_silu_mul(const void* gu, int64_t ld_gu, int inter, void* out, int64_t ld_out, int rows,
+                             hipStream_t stream) {
+  if (!gu || !out || inter < 1 || rows < 0 || ld_gu < 2 * (int64_t)inter || ld_out < inter) return EGPT_ERR_INVALID;
+  if (rows == 0) return EGPT_OK;
+  const int64_t total = (int64_t)rows * inter;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                     (const uint16_t*)gu, ld_gu, inter, (uint16_t*)out, ld_out, rows);
+  return EGPT_LAUNCH_STATUS();
+}
+
+extern "C" int egpt_embed(const int64_t* tokens, int rows, const void* table, int64_t ld_table, int vocab, void* out,
+                          int64_t ld_out, int n, hipStream_t stream) {
+  if (!tokens || !table || !out || rows < 0 || vocab < 1 || n < 1 || ld_table < n || ld_out < n)
+    return EGPT_ERR_INVALID;
+  if (rows == 0) return EGPT_OK;
+  dim3 grid((unsigned)((n + 255) / 256 < 8 ? (n + 255) / 256 : 8), (unsigned)rows);
+  hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, stream, tokens, (const uint16_t*)table, ld_table, vocab,
+                     (uint16_t*)out, ld_out, n);
+  return EGPT_LAUNCH_STATUS();
+}
+
+extern "C" int egpt_argmax_workspace(int n, size_t* bytes) {
+  if (!bytes || n < 1) return EGPT_ERR_INVALID;
+  *bytes = (size_t)kArgParts * (sizeof(float) + sizeof(int));
+  return EGPT_OK;
+}
+
+extern "C" int egpt_argmax(const void* logits, int n, void* workspace, size_t workspace_bytes, int64_t* token,
+                           int64_t* position, hipStream_t stream) {
+  if (!logits || !token || n < 1) return EGPT_ERR_INVALID;
+  size_t need = 0;
+  egpt_argmax_workspace(n, &need);
+  if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16) return EGPT_ERR_WORKSPACE;
+  const int per_block = (n + kArgParts - 1) / kArgParts;
+  const int parts = (n + per_block - 1) / per_block;
+  float* pv = (float*)workspace;
+  int* pi = (int*)((char*)workspace + kArgParts * sizeof(float));
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts), dim3(kArgThreads), 0, stream, (const uint16_t*)logits, n,
+                     per_block, pv, pi);
+  if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgThreads), 0, stream, pv, pi, parts, token, position);
+  return EGPT_LAUNCH_STATUS();
+}

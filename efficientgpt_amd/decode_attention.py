@@ -20,7 +20,7 @@ import torch
 
 from . import _lib
 
-_SUPPORTED_D = (64, 128)
+_SUPPORTED_D = (32, 64, 128)
 _SUPPORTED_GROUPS = (1, 2, 4, 8)
 
 
@@ -55,13 +55,16 @@ def _validate(q, k, v, position):
 
 
 def _aligned(t, dims):
-    """Last dim contiguous and every stride in `dims` a multiple of 16 bytes (16-byte lane loads)."""
+    """Last dim contiguous and every stride in `dims` a multiple of 16 bytes (16-byte lane loads).
+
+    A stride of 0 (a batch dimension expanded over one cache) is aligned.
+    """
     esz = t.element_size()
     return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
             and all((t.stride(i) * esz) % 16 == 0 for i in dims))
 
 
-def _run(q, k, v, position, nsplit):
+def _run(q, k, v, position, nsplit, scale=None):
     b, h, hkv, cap, d = _validate(q, k, v, position)
     if not _aligned(q, (0, 1)):
         q = q.contiguous()
@@ -84,7 +87,8 @@ def _run(q, k, v, position, nsplit):
                               position.data_ptr(), pos_stride,
                               out.data_ptr(), out.stride(0), out.stride(1),
                               ws.data_ptr(), ws.numel(),
-                              b, h, hkv, cap, d, nsplit, d ** -0.5, _lib.stream_ptr(q.device))
+                              b, h, hkv, cap, d, nsplit, d ** -0.5 if scale is None else float(scale),
+                              _lib.stream_ptr(q.device))
     _lib.check('egpt_decode_attn', st)
     return out
 

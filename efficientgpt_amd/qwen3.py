@@ -1,0 +1,370 @@
+"""Batch-1 Qwen3 int8 decode engine on the gfx950 kernels.
+
+The decode step of a Qwen3 decoder (transformers' models/qwen3/modeling_qwen3.py),
+every linear int8 weight-only, run entirely through libegpt_hip.so and captured as
+one graph: the host launches nothing per token but the graph replay. It is the
+MI355X counterpart of the reference's captured step (research/realmodel/fast_decode.py:
+GraphGreedyDecoder._step / _capture, :45-64) with the Inductor-compiled HF forward
+replaced by explicit kernels.
+
+Data layout in HBM (per layer, all device-resident for the life of the engine):
+  qkv_q   int8 [(Hq + 2 Hkv) * D, hidden]   q, k, v projections stacked by rows
+  qkv_s   fp32 [(Hq + 2 Hkv) * D]           their per-row scales (rows are independent,
+                                            so stacking is bit-identical to 3 GEMVs)
+  o_q     int8 [hidden, Hq * D]             o_proj
+  gu_q    int8 [2 * inter, hidden]          gate rows then up rows
+  down_q  int8 [hidden, inter]
+  k_cache, v_cache  bf16 [layers, Hkv, cap, D]  static cache, slot = position
+plus the bf16 embedding [vocab, hidden], the int8 lm_head (a tied head is an int8
+copy of the embedding, research/realmodel/int8_linear.py:154-155) and bf16 RoPE
+tables [cap, D] built with transformers' formula.
+
+Step (token t at position p; writes K/V slot p, attends to slots 0..p):
+  embed -> [add+]RMSNorm -> QKV GEMV -> q/k norm + RoPE + cache write -> split-K
+  attention + combine -> o GEMV -> add+RMSNorm -> gate_up GEMV -> SiLU*up ->
+  down GEMV -> ... -> add+final RMSNorm -> lm_head GEMV -> argmax (token, p + 1).
+Prefill runs the same kernels over all prompt rows (linears past 16 rows take the
+reference's dequantised GEMM formula, int8_linear.py:96-97), outside the graph.
+"""
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .int8_linear import MAX_DECODE_ROWS, quantize_weight
+
+LINEARS = ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj', 'self_attn.o_proj',
+           'mlp.gate_proj', 'mlp.up_proj', 'mlp.down_proj')
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    vocab: int
+    hidden: int
+    inter: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rope_theta: float = 1e6
+    rms_eps: float = 1e-6
+    tied: bool = True
+
+    @classmethod
+    def from_hf(cls, cfg):
+        rope = getattr(cfg, 'rope_parameters', None) or {}
+        theta = rope.get('rope_theta', getattr(cfg, 'rope_theta', 1e6))
+        head_dim = getattr(cfg, 'head_dim', None) or cfg.hidden_size // cfg.num_attention_heads
+        return cls(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers,
+                   cfg.num_attention_heads, cfg.num_key_value_heads, head_dim, float(theta), cfg.rms_norm_eps,
+                   bool(getattr(cfg, 'tie_word_embeddings', False)))
+
+    def weight_bytes(self):
+        """int8 linear bytes + fp32 scales streamed per decode step (lm_head included)."""
+        d = self.head_dim
+        per_layer_rows = (self.heads + 2 * self.kv_heads) * d + self.hidden + 2 * self.inter + self.hidden
+        per_layer = ((self.heads + 2 * self.kv_heads) * d * self.hidden + self.hidden * self.heads * d
+                     + 2 * self.inter * self.hidden + self.hidden * self.inter)
+        return (self.layers * per_layer + self.vocab * self.hidden,
+                4 * (self.layers * per_layer_rows + self.vocab))
+
+    def kv_bytes_per_slot(self):
+        return self.layers * self.kv_heads * self.head_dim * 2 * 2
+
+
+QWEN3_1_7B = Qwen3Config(vocab=151936, hidden=2048, inter=6144, layers=28, heads=16, kv_heads=8, head_dim=128)
+QWEN3_8B = Qwen3Config(vocab=151936, hidden=4096, inter=12288, layers=36, heads=32, kv_heads=8, head_dim=128,
+                       tied=False)
+
+
+def rope_tables(cfg, length, inv_freq=None):
+    """bf16 cos/sin [length, head_dim] with transformers' arithmetic (fp32 products, cos/sin, cast).
+
+    Built once on the host at engine construction; `inv_freq` overrides the fp32
+    formula (a transformers model cast with .to(bfloat16) carries a bf16 copy).
+    """
+    d = cfg.head_dim
+    if inv_freq is None:
+        inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float) / d))
+    inv_freq = inv_freq.detach().cpu().float()
+    pos = torch.arange(length, dtype=torch.float)
+    freqs = (inv_freq[None, :, None] @ pos[None, None, :]).transpose(1, 2)[0]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+
+
+def _as_int8(weights, name):
+    """(qweight, scale) of linear `name`, quantising a float weight if that is what is given."""
+    if name + '.qweight' in weights:
+        return weights[name + '.qweight'], weights[name + '.scale'].float()
+    return quantize_weight(weights[name + '.weight'])
+
+
+class Qwen3Int8Engine:
+    """Static-cache batch-1 Qwen3 decoder with int8 linears; one graph replay per token."""
+
+    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None):
+        if max_cache_len < 1:
+            raise ValueError('max_cache_len must be >= 1')
+        self.cfg, self.cap = cfg, int(max_cache_len)
+        self.device = torch.device(device)
+        dev, bf = self.device, torch.bfloat16
+        c = cfg
+        d = c.head_dim
+        self.n_qkv = (c.heads + 2 * c.kv_heads) * d
+
+        def put(t, dtype=None):
+            return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
+
+        self.layers = []
+        for i in range(c.layers):
+            p = f'model.layers.{i}.'
+            qs = [_as_int8(weights, p + n) for n in LINEARS]
+            L = {
+                'qkv_q': put(torch.cat([qs[0][0], qs[1][0], qs[2][0]])),
+                'qkv_s': put(torch.cat([qs[0][1], qs[1][1], qs[2][1]]), torch.float32),
+                'o_q': put(qs[3][0]), 'o_s': put(qs[3][1], torch.float32),
+                'gu_q': put(torch.cat([qs[4][0], qs[5][0]])),
+                'gu_s': put(torch.cat([qs[4][1], qs[5][1]]), torch.float32),
+                'down_q': put(qs[6][0]), 'down_s': put(qs[6][1], torch.float32),
+                'in_w': put(weights[p + 'input_layernorm.weight'], bf),
+                'post_w': put(weights[p + 'post_attention_layernorm.weight'], bf),
+                'qn_w': put(weights[p + 'self_attn.q_norm.weight'], bf),
+                'kn_w': put(weights[p + 'self_attn.k_norm.weight'], bf),
+            }
+            self.layers.append(L)
+            del qs
+        self.embed = put(weights['model.embed_tokens.weight'], bf)
+        self.norm_w = put(weights['model.norm.weight'], bf)
+        if 'lm_head.qweight' in weights or 'lm_head.weight' in weights:
+            hq, hs = _as_int8(weights, 'lm_head')
+        else:  # tied: int8 copy of the embedding, the embedding stays bf16
+            hq, hs = quantize_weight(self.embed)
+        self.head_q, self.head_s = put(hq), put(hs, torch.float32)
+        cos, sin = rope_tables(c, self.cap, inv_freq)
+        self.cos, self.sin = put(cos), put(sin)
+
+        # static state and activations
+        self.k_cache = torch.zeros(c.layers, c.kv_heads, self.cap, d, device=dev, dtype=bf)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.token = torch.zeros(1, dtype=torch.long, device=dev)
+        self.position = torch.zeros(1, dtype=torch.long, device=dev)
+        self.x = torch.zeros(1, c.hidden, device=dev, dtype=bf)
+        self.h = torch.zeros(1, c.hidden, device=dev, dtype=bf)
+        self.qkv = torch.zeros(1, self.n_qkv, device=dev, dtype=bf)
+        self.qrot = torch.zeros(1, c.heads * d, device=dev, dtype=bf)
+        self.attn = torch.zeros(1, c.heads * d, device=dev, dtype=bf)
+        self.o = torch.zeros(1, c.hidden, device=dev, dtype=bf)
+        self.gu = torch.zeros(1, 2 * c.inter, device=dev, dtype=bf)
+        self.act = torch.zeros(1, c.inter, device=dev, dtype=bf)
+        self.down = torch.zeros(1, c.hidden, device=dev, dtype=bf)
+        self.logits = torch.zeros(1, c.vocab, device=dev, dtype=bf)
+        lib = _lib.lib()
+        self.nsplit = lib.egpt_decode_attn_default_splits(1, c.kv_heads, self.cap)
+        need = ctypes.c_size_t()
+        _lib.check('egpt_decode_attn_workspace',
+                   lib.egpt_decode_attn_workspace(1, c.heads, c.kv_heads, self.cap, d, self.nsplit, need))
+        self.attn_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
+        _lib.check('egpt_argmax_workspace', lib.egpt_argmax_workspace(c.vocab, need))
+        self.arg_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
+        self.graph = None
+
+    # ------------------------------------------------------------------ construction helpers
+
+    @classmethod
+    @torch.no_grad()
+    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda'):
+        """Random-init weights N(0, std) (bf16, norms 1), quantised per output channel on the device."""
+        dev = torch.device(device)
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def randn(n, k):
+            return (torch.randn(n, k, generator=g, device=dev) * std).to(torch.bfloat16)
+
+        c = cfg
+        d = c.head_dim
+        dims = {'self_attn.q_proj': (c.heads * d, c.hidden), 'self_attn.k_proj': (c.kv_heads * d, c.hidden),
+                'self_attn.v_proj': (c.kv_heads * d, c.hidden), 'self_attn.o_proj': (c.hidden, c.heads * d),
+                'mlp.gate_proj': (c.inter, c.hidden), 'mlp.up_proj': (c.inter, c.hidden),
+                'mlp.down_proj': (c.hidden, c.inter)}
+        w = {'model.embed_tokens.weight': randn(c.vocab, c.hidden)}
+        ones = torch.ones(c.hidden, device=dev, dtype=torch.bfloat16)
+        ones_d = torch.ones(d, device=dev, dtype=torch.bfloat16)
+        for i in range(c.layers):
+            p = f'model.layers.{i}.'
+            for name, (n, k) in dims.items():
+                w[p + name + '.qweight'], w[p + name + '.scale'] = quantize_weight(randn(n, k))
+            w[p + 'input_layernorm.weight'] = ones
+            w[p + 'post_attention_layernorm.weight'] = ones
+            w[p + 'self_attn.q_norm.weight'] = ones_d
+            w[p + 'self_attn.k_norm.weight'] = ones_d
+        w['model.norm.weight'] = ones
+        if not c.tied:
+            w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(randn(c.vocab, c.hidden))
+        else:
+            w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(w['model.embed_tokens.weight'])
+        eng = cls(cfg, w, max_cache_len, device=dev)
+        eng.weights = w  # kept so a CPU oracle can be built from the very same tensors
+        return eng
+
+    @classmethod
+    @torch.no_grad()
+    def from_hf(cls, model, max_cache_len):
+        """Engine over a transformers Qwen3ForCausalLM (int8 linears taken as they are, float ones quantised)."""
+        cfg = Qwen3Config.from_hf(model.config)
+        sd = dict(model.state_dict())
+        if 'lm_head.qweight' not in sd and cfg.tied:
+            sd.pop('lm_head.weight', None)  # tied float head: quantise from the embedding
+        device = next(model.parameters()).device
+        return cls(cfg, sd, max_cache_len, device=device, inv_freq=model.model.rotary_emb.inv_freq)
+
+    # ------------------------------------------------------------------ kernels
+
+    def _stream(self):
+        return _lib.stream_ptr(self.device)
+
+    def _linear(self, x, q, s, out, rows):
+        """out[:rows] = int8 linear of x[:rows]; the reference's row rule (<= 16 rows: GEMV kernel)."""
+        if rows <= MAX_DECODE_ROWS:
+            _lib.check('egpt_int8_gemv', _lib.lib().egpt_int8_gemv(
+                x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), s.data_ptr(), out.data_ptr(), out.stride(0),
+                rows, q.shape[0], q.shape[1], self._stream()))
+        else:
+            out[:rows] = ((x[:rows] @ q.to(torch.bfloat16).t()).float() * s).to(torch.bfloat16)
+
+    def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first):
+        lib, c, L, st = _lib.lib(), self.cfg, self.layers[i], self._stream()
+        d = c.head_dim
+        if first:
+            _lib.check('egpt_rmsnorm', lib.egpt_rmsnorm(x.data_ptr(), x.stride(0), L['in_w'].data_ptr(), h.data_ptr(),
+                                                        h.stride(0), rows, c.hidden, c.rms_eps, st))
+        else:
+            _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
+                x.data_ptr(), x.stride(0), down.data_ptr(), down.stride(0), L['in_w'].data_ptr(), h.data_ptr(),
+                h.stride(0), rows, c.hidden, c.rms_eps, st))
+        self._linear(h, L['qkv_q'], L['qkv_s'], qkv, rows)
+        kc, vc = self.k_cache[i], self.v_cache[i]
+        _lib.check('egpt_qk_norm_rope', lib.egpt_qk_norm_rope(
+            qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), L['qn_w'].data_ptr(), L['kn_w'].data_ptr(),
+            self.cos.data_ptr(), self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(),
+            kc.stride(0), kc.stride(1), rows, c.heads, c.kv_heads, d, self.cap, c.rms_eps, st))
+        # attention: every query row is a batch row over the shared cache (batch stride 0)
+        if rows == 1:
+            nsplit, ws = self.nsplit, self.attn_ws
+        else:
+            nsplit = lib.egpt_decode_attn_default_splits(rows, c.kv_heads, self.cap)
+            need = ctypes.c_size_t()
+            _lib.check('egpt_decode_attn_workspace', lib.egpt_decode_attn_workspace(
+                rows, c.heads, c.kv_heads, self.cap, d, nsplit, need))
+            ws = torch.empty(need.value, device=self.device, dtype=torch.uint8)
+        _lib.check('egpt_decode_attn', lib.egpt_decode_attn(
+            _lib.EGPT_BF16, qrot.data_ptr(), qrot.stride(0), d,
+            kc.data_ptr(), 0, kc.stride(0), kc.stride(1),
+            vc.data_ptr(), 0, vc.stride(0), vc.stride(1),
+            positions.data_ptr(), pos_stride,
+            attn.data_ptr(), attn.stride(0), d,
+            ws.data_ptr(), ws.numel(), rows, c.heads, c.kv_heads, self.cap, d, nsplit, d ** -0.5, st))
+        self._linear(attn, L['o_q'], L['o_s'], o, rows)
+        _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
+            x.data_ptr(), x.stride(0), o.data_ptr(), o.stride(0), L['post_w'].data_ptr(), h.data_ptr(), h.stride(0),
+            rows, c.hidden, c.rms_eps, st))
+        self._linear(h, L['gu_q'], L['gu_s'], gu, rows)
+        _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
+                                                      act.stride(0), rows, st))
+        self._linear(act, L['down_q'], L['down_s'], down, rows)
+
+    def _head(self, x, down, h):
+        """Final residual add + norm of one row, lm_head GEMV, argmax into token, position += 1."""
+        lib, c, st = _lib.lib(), self.cfg, self._stream()
+        _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
+            x.data_ptr(), x.stride(0), down.data_ptr(), down.stride(0), self.norm_w.data_ptr(), h.data_ptr(),
+            h.stride(0), 1, c.hidden, c.rms_eps, st))
+        self._linear(h, self.head_q, self.head_s, self.logits, 1)
+        _lib.check('egpt_argmax', lib.egpt_argmax(self.logits.data_ptr(), c.vocab, self.arg_ws.data_ptr(),
+                                                  self.arg_ws.numel(), self.token.data_ptr(),
+                                                  self.position.data_ptr(), st))
+
+    # ------------------------------------------------------------------ public API
+
+    @torch.inference_mode()
+    def reset(self):
+        """Clear the cache and the token / position state (in place: captured addresses stay valid)."""
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+        self.token.zero_()
+        self.position.zero_()
+
+    @torch.inference_mode()
+    def step(self):
+        """One decode step on the current stream: consumes self.token at self.position, writes the next token."""
+        lib, c = _lib.lib(), self.cfg
+        _lib.check('egpt_embed', lib.egpt_embed(self.token.data_ptr(), 1, self.embed.data_ptr(), self.embed.stride(0),
+                                                c.vocab, self.x.data_ptr(), self.x.stride(0), c.hidden,
+                                                self._stream()))
+        for i in range(c.layers):
+            self._layer(i, 1, self.x, self.h, self.qkv, self.qrot, self.attn, self.o, self.gu, self.act, self.down,
+                        self.position, 0, first=(i == 0))
+        self._head(self.x, self.down, self.h)
+
+    @torch.inference_mode()
+    def prefill(self, tokens, pos0=0):
+        """Run prompt ids (1-D, on any device) at positions pos0.. through the model; sets token = greedy next
+        token and position = pos0 + len(tokens). Returns the last row's logits (bf16 [vocab])."""
+        c, dev, bf = self.cfg, self.device, torch.bfloat16
+        ids = torch.as_tensor(tokens, dtype=torch.long).reshape(-1).to(dev)
+        t = ids.numel()
+        if t < 1:
+            raise ValueError('prefill needs at least one token')
+        if pos0 + t > self.cap:
+            raise ValueError('prompt exceeds the cache capacity')
+        positions = torch.arange(pos0, pos0 + t, device=dev, dtype=torch.long)
+        x = torch.empty(t, c.hidden, device=dev, dtype=bf)
+        h = torch.empty_like(x)
+        qkv = torch.empty(t, self.n_qkv, device=dev, dtype=bf)
+        qrot = torch.empty(t, c.heads * c.head_dim, device=dev, dtype=bf)
+        attn = torch.empty_like(qrot)
+        o = torch.empty_like(x)
+        gu = torch.empty(t, 2 * c.inter, device=dev, dtype=bf)
+        act = torch.empty(t, c.inter, device=dev, dtype=bf)
+        down = torch.empty_like(x)
+        lib = _lib.lib()
+        _lib.check('egpt_embed', lib.egpt_embed(ids.data_ptr(), t, self.embed.data_ptr(), self.embed.stride(0),
+                                                c.vocab, x.data_ptr(), x.stride(0), c.hidden, self._stream()))
+        for i in range(c.layers):
+            self._layer(i, t, x, h, qkv, qrot, attn, o, gu, act, down, positions, 1, first=(i == 0))
+        self.position.fill_(pos0 + t - 1)  # argmax advances it to pos0 + t
+        self._head(x[t - 1:], down[t - 1:], h[t - 1:])
+        return self.logits[0]
+
+    @torch.inference_mode()
+    def capture(self):
+        """Capture step() as one graph (warm-up on a side stream first, as graph capture requires).
+
+        Runs under inference mode like every other engine entry point, so the capture
+        never mixes inference and normal tensors (torch's graph capture updates its
+        RNG state tensors in place).
+        """
+        saved = (self.token.clone(), self.position.clone(), self.x.clone())
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            self.step()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        torch.cuda.synchronize(self.device)
+        self.token.copy_(saved[0])
+        self.position.copy_(saved[1])
+        self.x.copy_(saved[2])
+        self.graph = g
+        return g
+
+    @torch.inference_mode()
+    def replay(self):
+        if self.graph is None:
+            self.capture()
+        self.graph.replay()

@@ -74,7 +74,7 @@ int egpt_int8_gemv_splitk(const void *x, int64_t ldx, const int8_t *w, int64_t l
  *   out [B, Hq, 1, D]     strides (o_sb, o_sh), in the input dtype.
  * Query head h reads kv head h / (Hq / Hkv). fp32 math, online softmax per split,
  * partials (max, sum, acc[D]) reduced in fp32. dtype: EGPT_F32 / EGPT_BF16 / EGPT_F16.
- * D in {64, 128}; Hq / Hkv in {1, 2, 4, 8}. nsplit <= 0 picks the default.
+ * D in {32, 64, 128}; Hq / Hkv in {1, 2, 4, 8}. nsplit <= 0 picks the default.
  * With Hkv == Hq this is the reference's MHA contract.
  * Replaces _split_kernel + _combine_kernel and the NSPLIT choice
  * (research/phase5/decode_attention.py:22-71, :74-103); nsplit 1 is the
@@ -91,6 +91,51 @@ int egpt_decode_attn(int dtype,
                      void *workspace, size_t workspace_bytes,
                      int B, int Hq, int Hkv, int cap, int D, int nsplit, float scale,
                      hipStream_t stream);
+
+/*
+ * Decode-step kernels of the Qwen3 layer around the two hot kernels. They replace
+ * the elementwise work the reference leaves to transformers' modules compiled by
+ * Inductor inside its graph step (research/realmodel/fast_decode.py:42-49); the
+ * arithmetic is transformers' bf16 Qwen3 (models/qwen3/modeling_qwen3.py).
+ * Activations are bf16 [rows, n] with row strides ld*.
+ */
+
+/* y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), fp32 statistics
+ * (Qwen3RMSNorm, modeling_qwen3.py:30-46). n <= 16384. */
+int egpt_rmsnorm(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy, int rows, int n, float eps,
+                 hipStream_t stream);
+
+/* Residual add then RMSNorm: x = bf16(x + a) in place, y = RMSNorm(x)
+ * (the `residual + hidden_states` / next-norm pair of Qwen3DecoderLayer, modeling_qwen3.py:285-322). */
+int egpt_add_rmsnorm(void *x, int64_t ldx, const void *a, int64_t lda, const void *w, void *y, int64_t ldy,
+                     int rows, int n, float eps, hipStream_t stream);
+
+/* q_norm / k_norm (RMSNorm over head_dim), RoPE with bf16 cos/sin tables [cap, D],
+ * and the static-cache write of the new key and value at slot positions[r]
+ * (Qwen3Attention.forward up to past_key_values.update, modeling_qwen3.py:252-263;
+ * the reference's `keys.index_copy_(2, position, k)`, research/phase5/compiled_baseline.py:44-45).
+ * qkv rows are [q (Hq*D) | k (Hkv*D) | v (Hkv*D)]; rotated queries go to q_out [rows, Hq*D];
+ * caches are [Hkv, cap, D] with strides (cache_head_stride, cache_slot_stride). D in {32, 64, 128}. */
+int egpt_qk_norm_rope(const void *qkv, int64_t ld_qkv, const int64_t *positions, const void *q_norm_w,
+                      const void *k_norm_w, const void *cos_t, const void *sin_t, void *q_out, int64_t ld_q,
+                      void *k_cache, void *v_cache, int64_t cache_head_stride, int64_t cache_slot_stride,
+                      int rows, int Hq, int Hkv, int D, int cap, float eps, hipStream_t stream);
+
+/* act = bf16(bf16(silu(gate)) * up) over rows laid out [gate (inter) | up (inter)]
+ * (Qwen3MLP, modeling_qwen3.py:49-62). */
+int egpt_silu_mul(const void *gu, int64_t ld_gu, int inter, void *out, int64_t ld_out, int rows,
+                  hipStream_t stream);
+
+/* out[r] = table[tokens[r]] (embed_tokens gather; ids clamped to [0, vocab)). */
+int egpt_embed(const int64_t *tokens, int rows, const void *table, int64_t ld_table, int vocab, void *out,
+               int64_t ld_out, int n, hipStream_t stream);
+
+/* Greedy pick: *token = first index of the largest bf16 logit (torch.argmax), and
+ * *position += 1 when position is non-null: the token/position update of the
+ * reference's graph step (research/realmodel/fast_decode.py:48-49). */
+int egpt_argmax_workspace(int n, size_t *bytes);
+int egpt_argmax(const void *logits, int n, void *workspace, size_t workspace_bytes, int64_t *token,
+                int64_t *position, hipStream_t stream);
 
 #ifdef __cplusplus
 }

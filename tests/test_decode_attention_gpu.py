@@ -4,8 +4,12 @@ Mirrors research/phase5/test_graph_gpu.py:205-261 and :302-398 (fp32 / bf16 / fp
 inputs, positions {0, cap-1, cap/2, random per row}, x8 scaled logits, NaN-poisoned
 slots past the position, non-contiguous K/V, dispatch) and extends them to grouped
 query heads at the Qwen3 shapes (16 query / 8 kv heads, D = 128, L up to 32768).
-Bounds: no worse than 2x the same-dtype masked SDPA error against fp64 (SDPA run on
-the CPU), with the reference's floors, and within 2e-2 relative everywhere.
+Bounds: no worse than 2x the error against fp64 of the same-dtype masked SDPA (run on
+the CPU) or of the reference's own split-K algorithm in fp32 (the oracle's
+restatement of research/phase5/decode_attention.py:31-71), with the reference's
+floors (1e-6 fp32, 1e-3 bf16/fp16), and within 2e-2 relative everywhere. The second
+yardstick is the reference's own practice (research/phase5/test_graph_gpu.py:305-307
+bounds by 1.25x its accepted split-K kernel) for cases where SDPA is unusually accurate.
 """
 
 import numpy as np
@@ -31,6 +35,12 @@ def sdpa_err_cpu(q, k, v, pos, truth):
     return float((out.double().numpy() - truth).__abs__().max())
 
 
+def splitk_err(q, k, v, pos, truth):
+    """max |reference split-K algorithm in fp32 - truth| (K/V in the input dtype, math in fp32)."""
+    got = oatt.attention_splitk(q.float().numpy(), k.float().numpy(), v.float().numpy(), pos.numpy())
+    return float(np.abs(got.astype(np.float64) - truth).max())
+
+
 def run_case(b, hq, hkv, cap, d, dtype, pos, scale=1.0, seed=0, floor=None, config=None):
     from efficientgpt_amd.decode_attention import decode_attention
     g = torch.Generator().manual_seed(seed)
@@ -44,7 +54,10 @@ def run_case(b, hq, hkv, cap, d, dtype, pos, scale=1.0, seed=0, floor=None, conf
     err = float(np.abs(out.double().cpu().numpy() - truth).max())
     if floor is None:
         floor = 1e-6 if dtype == torch.float32 else 1e-3
-    bound = max(2 * sdpa_err_cpu(q, k, v, pos, truth), floor)
+    yard = sdpa_err_cpu(q, k, v, pos, truth)
+    if dtype == torch.float32 and cap <= 512:
+        yard = max(yard, splitk_err(q, k, v, pos, truth))
+    bound = max(2 * yard, floor)
     assert err <= bound, (b, hq, hkv, cap, d, dtype, pos.tolist(), err, bound)
     assert err <= 2e-2 * max(float(np.abs(truth).max()), 1e-30)
     return out
@@ -53,10 +66,8 @@ def run_case(b, hq, hkv, cap, d, dtype, pos, scale=1.0, seed=0, floor=None, conf
 @pytest.mark.parametrize('batch,cap', [(1, 80), (1, 256), (16, 128), (16, 256), (3, 37), (2, 2)])
 @pytest.mark.parametrize('scale', [1.0, 8.0])
 def test_mha_fp32_against_fp64(batch, cap, scale):
-    # floor 2e-6: fp32 math with a different summation order than SDPA; the reference's 1e-6 floor
-    # is set for its Triton kernel on NVIDIA and the CPU SDPA used here as yardstick is tighter
     for pos in ([0], [cap - 1], [cap // 2], torch.randint(0, cap, (batch,), generator=torch.Generator().manual_seed(batch)).tolist()):
-        run_case(batch, 6, 6, cap, 64, torch.float32, pos, scale=scale, seed=cap, floor=2e-6)
+        run_case(batch, 6, 6, cap, 64, torch.float32, pos, scale=scale, seed=cap)
 
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
@@ -75,7 +86,7 @@ def test_qwen3_gqa_shapes_bf16(L):
 @pytest.mark.parametrize('hq,hkv', [(32, 8), (8, 1), (4, 2)])
 def test_other_groupings(hq, hkv):
     run_case(2, hq, hkv, 300, 128, torch.bfloat16, [5, 299], seed=hq)
-    run_case(1, hq, hkv, 100, 64, torch.float32, [77], seed=hkv, floor=2e-6)
+    run_case(1, hq, hkv, 100, 64, torch.float32, [77], seed=hkv)
 
 
 def test_split_count_invariance_and_single_pass():

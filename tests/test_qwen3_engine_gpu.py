@@ -1,0 +1,177 @@
+"""Qwen3 int8 decode engine and graph decoder vs the CPU oracle.
+
+Mirrors research/realmodel/test_fast_decode.py (tiny random Qwen3 with 4 query /
+2 kv heads, prompts of 1, 5 and 37 tokens, 40 new tokens, non-degenerate output,
+EOS exactness without leaking run-ahead tokens, cache reset between requests,
+guards) with the CPU oracle (oracle/qwen3.py, pinned against transformers) as the
+reference, and adds a Qwen3-shaped layer at the real head geometry (D = 128).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.qwen3 import Qwen3Oracle, Qwen3Shape, TINY, quantize_weights, random_weights
+from tests.near_tie import near_tie_match
+
+pytestmark = pytest.mark.gpu
+
+# Qwen3-1.7B head geometry (16 q / 8 kv heads, D = 128) at a small width and depth
+SMALL = Qwen3Shape(vocab=2048, hidden=512, inter=1024, layers=3, heads=16, kv_heads=8, head_dim=128)
+
+
+def build(shape, seed, std, cap):
+    from efficientgpt_amd.qwen3 import Qwen3Config, Qwen3Int8Engine
+    w = quantize_weights(random_weights(shape, seed=seed, std=std, norm_jitter=0.1), shape)
+    cfg = Qwen3Config(shape.vocab, shape.hidden, shape.inter, shape.layers, shape.heads, shape.kv_heads,
+                      shape.head_dim, shape.rope_theta, shape.rms_eps, shape.tied)
+    eng = Qwen3Int8Engine(cfg, {k: v.cuda() for k, v in w.items()}, cap)
+    orc = Qwen3Oracle(shape, w, dtype=torch.bfloat16, cap=cap)
+    return eng, orc
+
+
+def oracle_greedy_with_margins(orc, prompt, n):
+    toks, margins = orc.greedy(prompt, n, with_margins=True)
+    orc.reset()
+    tops, logits, pos = [], orc.forward(prompt, 0), len(prompt)
+    for i in range(n):
+        tops.append(float(logits.float().max()))
+        if i + 1 < n:
+            logits = orc.forward([toks[i]], pos)
+            pos += 1
+    return toks, margins, tops
+
+
+@pytest.mark.parametrize('shape,std', [(TINY, 0.2), (SMALL, 0.15)])
+def test_prefill_logits_match_oracle(shape, std):
+    eng, orc = build(shape, seed=1, std=std, cap=96)
+    g = torch.Generator().manual_seed(2)
+    for p in (1, 5, 17, 37):
+        prompt = torch.randint(0, shape.vocab, (p,), generator=g)
+        eng.reset()
+        got = eng.prefill(prompt).float().cpu()
+        orc.reset()
+        want = orc.forward(prompt, 0).float()
+        rel = float((got - want).abs().max() / want.abs().max())
+        assert rel < 2e-2, (p, rel)
+        assert int(torch.argmax(got)) == int(torch.argmax(want)) or \
+            float(want.max() - want[int(torch.argmax(got))]) < 0.1 * float(want.abs().max()), p
+
+
+@pytest.mark.parametrize('shape,std', [(TINY, 0.2), (SMALL, 0.15)])
+def test_graph_decoder_greedy_matches_oracle(shape, std):
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    eng, orc = build(shape, seed=3, std=std, cap=128)
+    dec = GraphGreedyDecoder(eng, max_cache_len=128)
+    g = torch.Generator().manual_seed(1)
+    agree = total = 0
+    for p in (1, 5, 37):
+        x = torch.randint(0, shape.vocab, (1, p), generator=g)
+        got, st = dec.generate(x.cuda(), 40)
+        assert st['tokens'] == 40 and len(got) == 40
+        assert len(set(got)) > 8, 'degenerate model output would make equality trivial'
+        ref, margins, tops = oracle_greedy_with_margins(orc, x[0], 40)
+        ok, where = near_tie_match(ref, got, margins, tops)
+        assert ok, (p, where, ref[:where + 1] if where is not None else None, got[:where + 1] if where else None)
+        agree += sum(a == b for a, b in zip(ref, got))
+        total += 40
+    assert agree / total >= 0.9
+
+
+def test_graph_replay_equals_eager_step():
+    eng, _ = build(SMALL, seed=5, std=0.05, cap=64)
+    prompt = torch.arange(7) * 13
+    eng.reset()
+    eng.prefill(prompt)
+    eager = []
+    for _ in range(10):
+        eng.step()
+        eager.append(int(eng.token))
+    eng.capture()
+    eng.reset()
+    eng.prefill(prompt)
+    graphed = []
+    for _ in range(10):
+        eng.replay()
+        graphed.append(int(eng.token))
+    assert graphed == eager
+
+
+def test_eos_stops_exactly_and_never_leaks_lookahead_tokens():
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    eng, _ = build(TINY, seed=7, std=0.2, cap=128)
+    dec = GraphGreedyDecoder(eng, max_cache_len=128, lookahead=8)
+    x = torch.randint(0, 512, (1, 7), generator=torch.Generator().manual_seed(2)).cuda()
+    full, _ = dec.generate(x, 60)
+    k = max(i for i in range(len(full)) if full[i] not in full[:i])
+    assert k > 10, 'EOS must fall well past the first lookahead window'
+    streamed = []
+    got, st = dec.generate(x, 60, eos_ids={full[k]}, on_token=streamed.append)
+    assert got == full[:k + 1]
+    assert streamed == got
+    again, _ = dec.generate(x, 60)
+    assert again == full
+
+
+def test_guards():
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    eng, _ = build(TINY, seed=0, std=0.2, cap=32)
+    dec = GraphGreedyDecoder(eng, max_cache_len=32)
+    with pytest.raises(ValueError):
+        dec.generate(torch.zeros((1, 20), dtype=torch.long, device='cuda'), 20)
+    with pytest.raises(ValueError):
+        dec.generate(torch.zeros((2, 4), dtype=torch.long, device='cuda'), 4)
+    with pytest.raises(ValueError):
+        dec.generate(torch.zeros((1, 4), dtype=torch.long, device='cuda'), 0)
+    out, st = dec.generate(torch.zeros((1, 4), dtype=torch.long, device='cuda'), 3)
+    assert (len(out), st['tokens']) == (3, 3)
+    assert 'capture_s' in st
+
+
+def test_transformers_model_int8_through_graph_decoder():
+    """A transformers Qwen3 quantised with quantize_model decodes through the engine like the oracle."""
+    transformers = pytest.importorskip('transformers')
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    from efficientgpt_amd.int8_linear import quantize_model
+    torch.manual_seed(0)
+    cfg = transformers.Qwen3Config(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                                   max_position_embeddings=256, tie_word_embeddings=True, initializer_range=0.2)
+    model = transformers.Qwen3ForCausalLM(cfg).cuda().to(torch.bfloat16).eval()
+    quantize_model(model)
+    sd = {k: v.cpu() for k, v in model.state_dict().items()}
+    orc = Qwen3Oracle(TINY, sd, dtype=torch.bfloat16, cap=128, inv_freq=model.model.rotary_emb.inv_freq)
+    dec = GraphGreedyDecoder(model, max_cache_len=128)
+    g = torch.Generator().manual_seed(1)
+    for p in (1, 5, 37):
+        x = torch.randint(0, 512, (1, p), generator=g)
+        got, _ = dec.generate(x.cuda(), 40)
+        assert len(set(got)) > 8
+        ref, margins, tops = oracle_greedy_with_margins(orc, x[0], 40)
+        ok, where = near_tie_match(ref, got, margins, tops)
+        assert ok, (p, where)
+
+
+def test_hf_attention_adapter_matches_oracle_attention():
+    """transformers with attn_implementation 'egpt_decode' (the HIP kernel) vs the fp32 oracle attention."""
+    transformers = pytest.importorskip('transformers')
+    from efficientgpt_amd import hf
+    hf.register()
+    torch.manual_seed(0)
+    cfg = transformers.Qwen3Config(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                                   max_position_embeddings=256, tie_word_embeddings=True, initializer_range=0.2,
+                                   attn_implementation=hf.NAME)
+    model = transformers.Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    orc = Qwen3Oracle(TINY, sd, dtype=torch.bfloat16, cap=128, inv_freq=model.model.rotary_emb.inv_freq)
+    model = model.cuda()
+    g = torch.Generator().manual_seed(4)
+    for p in (1, 6, 30):
+        x = torch.randint(0, 512, (1, p), generator=g)
+        with torch.no_grad():
+            got = model.generate(input_ids=x.cuda(), attention_mask=torch.ones_like(x).cuda(), max_new_tokens=20,
+                                 min_new_tokens=20, do_sample=False, pad_token_id=0)[0, p:].tolist()
+        ref, margins, tops = oracle_greedy_with_margins(orc, x[0], 20)
+        ok, where = near_tie_match(ref, got, margins, tops)
+        assert ok, (p, where)
