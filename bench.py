@@ -101,11 +101,19 @@ def gemv_roofline(eng, reps=20):
             'gemv_ms_per_step': round(per_step_s * 1e3, 4)}
 
 
+def host_threads():
+    """CPU threads this process may use: OMP_NUM_THREADS if set, else the cores in its affinity mask."""
+    env = os.environ.get('OMP_NUM_THREADS')
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0)) or 1
+
+
 def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
     """The CPU oracle on the same weights: prefill the prompt, then n_tokens greedy steps."""
     from oracle.qwen3 import Qwen3Oracle, Qwen3Shape
     c = eng.cfg
-    torch.set_num_threads(os.cpu_count() or 1)
+    torch.set_num_threads(host_threads())
     shape = Qwen3Shape(c.vocab, c.hidden, c.inter, c.layers, c.heads, c.kv_heads, c.head_dim, c.rope_theta,
                        c.rms_eps, c.tied)
     w = {k: v.cpu() for k, v in eng.weights.items()}
