@@ -48,7 +48,28 @@ SIGNATURES = {
     'egpt_embed': (_c_int, [_c_vp, _c_int, _c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_int, _c_vp]),
     'egpt_argmax_workspace': (_c_int, [_c_int, ctypes.POINTER(_c_size)]),
     'egpt_argmax': (_c_int, [_c_vp, _c_int, _c_vp, _c_size, _c_vp, _c_vp, _c_vp]),
+    'egpt_qwen3_step_workspace': (_c_int, [_c_vp, ctypes.POINTER(_c_size)]),
+    'egpt_qwen3_decode_step': (_c_int, [_c_vp, _c_vp]),
 }
+
+_LAYER_FIELDS = ('qkv_w', 'qkv_s', 'o_w', 'o_s', 'gu_w', 'gu_s', 'down_w', 'down_s', 'in_norm', 'post_norm',
+                 'q_norm', 'k_norm', 'k_cache', 'v_cache')
+
+
+class Qwen3Layer(ctypes.Structure):
+    """egpt_qwen3_layer: device pointers of one decoder layer."""
+    _fields_ = [(name, _c_vp) for name in _LAYER_FIELDS]
+
+
+class Qwen3Step(ctypes.Structure):
+    """egpt_qwen3_step: shapes, weights, state and workspace of one fused decode step."""
+    _fields_ = ([(name, _c_int) for name in ('layers', 'hidden', 'inter', 'heads', 'kv_heads', 'head_dim', 'vocab',
+                                             'cap', 'nsplit')]
+                + [('eps', _c_f)]
+                + [(name, _c_vp) for name in ('layer', 'embed', 'final_norm', 'head_w', 'head_s', 'rope_cos',
+                                              'rope_sin', 'token', 'position', 'x', 'qkv', 'attn', 'act', 'logits',
+                                              'workspace')]
+                + [('workspace_bytes', _c_size)])
 
 _lib = None
 

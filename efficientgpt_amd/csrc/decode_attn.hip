@@ -6,32 +6,12 @@
 // device, so a captured graph keeps working as the sequence grows). Each block
 // owns one (b, kv head, split) and serves all G query heads of the group, so
 // every K/V byte is read once. A second kernel merges the per-split partial
-// softmax states.
-//
-// Semantics follow the reference's Triton pair (research/phase5/decode_attention.py:
-// _split_kernel :22-56, _combine_kernel :59-71): scores (q . k) * scale in fp32,
-// an fp32 online softmax per split keeping (max, sum, acc[D]), and the combine
-//   w_i = exp(m_i - max_j m_j),  out = sum_i w_i acc_i / sum_i w_i l_i,
-// where empty splits carry m = -inf and weight 0. Only slots <= position[b] are
-// ever loaded. Exponentials are exp2((x - max) * log2 e): the same function as
-// the reference's exp, rounded relative to the max-subtracted logit; the
-// summation order differs from SDPA, so results are not bit-exact against it.
-//
-// Layout inside a block (256 threads, 4 wavefronts): one 16-byte load per lane
-// covers EPL = 16 / sizeof(T) elements of a row, LPS = D / EPL lanes cover one
-// slot (16 lanes for bf16 with D = 128), so a wavefront reads 64 / LPS
-// consecutive slots (1 KiB) per load. Each LPS-lane group runs its own online
-// softmax over every NG-th slot of the split (NG = 256 / LPS groups); the
-// groups are merged by cross-lane butterflies within a wavefront, then the four
-// wavefronts through LDS.
-#include "common.h"
+// softmax states. The arithmetic lives in attn_core.h; its summation order
+// differs from SDPA, so results are not bit-exact against it.
+#include "attn_core.h"
 
 namespace egpt {
 namespace {
-
-constexpr int kAttnThreads = 256;
-constexpr int kUnroll = 4;  // slots per group per iteration; double-buffered, so 2 x 4 K and V rows in flight
-constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
@@ -39,15 +19,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
     int64_t k_sn, const T* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
     const int64_t* __restrict__ position, int64_t pos_stride, float* __restrict__ ws_m, float* __restrict__ ws_l,
     float* __restrict__ ws_acc, int Hkv, int cap, int nsplit, float scale) {
-  constexpr int EPL = 16 / Elem<T>::kBytes;  // elements per 16-byte lane load
-  constexpr int LPS = D / EPL;               // lanes per slot
-  constexpr int NG = kAttnThreads / LPS;     // independent softmax streams per block
-  static_assert(LPS >= 1 && LPS <= 64 && (kWave % LPS) == 0, "unsupported head dim / dtype");
-
-  const int tid = threadIdx.x;
-  const int grp = tid / LPS;
-  const int sub = tid % LPS;
-  const int d0 = sub * EPL;
+  constexpr int EPL = AttnGeom<T, D>::EPL;
+  constexpr int LPS = AttnGeom<T, D>::LPS;
+  const int d0 = (threadIdx.x % LPS) * EPL;
   const int bh = blockIdx.x;  // b * Hkv + kv head
   const int b = bh / Hkv;
   const int hk = bh % Hkv;
@@ -56,162 +30,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
 
   int64_t len = position[(int64_t)b * pos_stride] + 1;
   len = len < 1 ? 1 : (len > cap ? cap : len);
-  const int64_t chunk = (len + nsplit - 1) / nsplit;
-  const int64_t start = (int64_t)split * chunk;
-  const int64_t end = start + chunk < len ? start + chunk : len;
+  int64_t start, end;
+  attn_split_range(len, nsplit, split, start, end);
 
-  // Query heads of this group in fp32.
   float qf[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const T* qp = q + (int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d0;
     Elem<T>::unpack(ld16(qp), qf[g]);
   }
-
-  float m[G], l[G], acc[G][EPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
-  }
-
-  const T* kbase = k + (int64_t)b * k_sb + (int64_t)hk * k_sh + d0;
-  const T* vbase = v + (int64_t)b * v_sb + (int64_t)hk * v_sh + d0;
-  constexpr int64_t kStep = (int64_t)NG * kUnroll;  // slots one group advances per iteration
-
-  // Register double buffer: the loads of iteration i+1 are issued before the
-  // arithmetic of iteration i, so each wavefront keeps 2 * kUnroll K and V rows
-  // in flight instead of waiting on every round trip.
-  u32x4 kr[kUnroll], vr[kUnroll];
-  auto issue = [&](int64_t base, u32x4* kd, u32x4* vd) {
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t n = base + (int64_t)u * NG;
-      const int64_t nn = n < end ? n : base;  // never touch slots past the live range
-      kd[u] = ld16(kbase + nn * k_sn);
-      vd[u] = ld16(vbase + nn * v_sn);
-    }
-  };
-  int64_t n0 = start + grp;
-  if (n0 < end) issue(n0, kr, vr);
-  for (; n0 < end; n0 += kStep) {
-    u32x4 kc[kUnroll], vc[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      kc[u] = kr[u];
-      vc[u] = vr[u];
-    }
-    if (n0 + kStep < end) issue(n0 + kStep, kr, vr);
-
-    float s[kUnroll][G];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const bool valid = n0 + (int64_t)u * NG < end;
-      float kf[EPL];
-      Elem<T>::unpack(kc[u], kf);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float p = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], kf[e], p);
-        p = group_sum<LPS>(p) * scale;  // the reference's fp32 logit: (q . k) * scale
-        s[u][g] = valid ? p : -INFINITY;
-      }
-    }
-    float vf[kUnroll][EPL];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) Elem<T>::unpack(vc[u], vf[u]);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mt = m[g];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) mt = fmaxf(mt, s[u][g]);
-      // slot n0 is always valid, so mt is finite; exp(x) = exp2(x * log2 e) after
-      // the max is subtracted, so the rounding is relative to the small difference
-      const float alpha = exp2f((m[g] - mt) * kLog2e);
-      float p[kUnroll];
-      float psum = 0.f;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        p[u] = exp2f((s[u][g] - mt) * kLog2e);  // 0 for invalid slots
-        psum += p[u];
-      }
-      l[g] = l[g] * alpha + psum;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        float a = acc[g][e] * alpha;
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) a = fmaf(p[u], vf[u][e], a);
-        acc[g][e] = a;
-      }
-      m[g] = mt;
-    }
-  }
-
-  // Merge the groups of each wavefront: butterflies across groups (lane
-  // distance LPS, 2*LPS, ...). Both partners end with the merged state.
-#pragma unroll
-  for (int off = LPS; off < kWave; off *= 2) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mo = __shfl_xor(m[g], off, kWave);
-      const float lo = __shfl_xor(l[g], off, kWave);
-      const float mx = fmaxf(m[g], mo);
-      const float ws = mx == -INFINITY ? 0.f : exp2f((m[g] - mx) * kLog2e);
-      const float wo = mx == -INFINITY ? 0.f : exp2f((mo - mx) * kLog2e);
-      l[g] = l[g] * ws + lo * wo;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float ao = __shfl_xor(acc[g][e], off, kWave);
-        acc[g][e] = acc[g][e] * ws + ao * wo;
-      }
-      m[g] = mx;
-    }
-  }
-
-  // Merge the 4 wavefronts through LDS and write this split's partial state.
-  constexpr int kWaves = kAttnThreads / kWave;
-  __shared__ float sm_m[kWaves][G];
-  __shared__ float sm_l[kWaves][G];
-  __shared__ float sm_acc[kWaves][G][D];
-  const int wave = tid / kWave;
-  const int lane = tid % kWave;
-  if (lane < LPS) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) sm_acc[wave][g][d0 + e] = acc[g][e];
-      if (lane == 0) {
-        sm_m[wave][g] = m[g];
-        sm_l[wave][g] = l[g];
-      }
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < G * D; i += kAttnThreads) {
-    const int g = i / D;
-    const int d = i % D;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kWaves; ++j) mx = fmaxf(mx, sm_m[j][g]);
-    float a = 0.f, ls = 0.f;
-    if (mx != -INFINITY) {
-#pragma unroll
-      for (int j = 0; j < kWaves; ++j) {
-        const float wj = exp2f((sm_m[j][g] - mx) * kLog2e);
-        a = fmaf(wj, sm_acc[j][g][d], a);
-        ls = fmaf(wj, sm_l[j][g], ls);
-      }
-    }
-    const int64_t slot = ((int64_t)b * Hq + hk * G + g) * nsplit + split;
-    ws_acc[slot * D + d] = a;
-    if (d == 0) {
-      ws_m[slot] = mx;
-      ws_l[slot] = ls;
-    }
-  }
+  attn_partial<T, D, G>(qf, k + (int64_t)b * k_sb + (int64_t)hk * k_sh, k_sn, v + (int64_t)b * v_sb + (int64_t)hk * v_sh,
+                        v_sn, start, end, scale, ws_m, ws_l, ws_acc, ((int64_t)b * Hq + hk * G) * nsplit + split,
+                        nsplit);
 }
 
 // Partial-softmax reduce: one block per (b, query head), one thread per d.
@@ -224,20 +54,9 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict
   const int b = bh / Hq;
   const int h = bh % Hq;
   const int d = threadIdx.x;
-  const float* mrow = ws_m + (int64_t)bh * nsplit;
-  const float* lrow = ws_l + (int64_t)bh * nsplit;
-  const float* arow = ws_acc + (int64_t)bh * nsplit * D;
-  float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, mrow[s]);
-  float a = 0.f, ls = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float ms = mrow[s];
-    if (ms == -INFINITY) continue;  // empty split: weight 0
-    const float wgt = exp2f((ms - mx) * kLog2e);
-    a = fmaf(wgt, arow[(int64_t)s * D + d], a);
-    ls = fmaf(wgt, lrow[s], ls);
-  }
-  Elem<T>::store1(out + (int64_t)b * o_sb + (int64_t)h * o_sh + d, a / ls);
+  const float r = attn_combine_one(ws_m + (int64_t)bh * nsplit, ws_l + (int64_t)bh * nsplit,
+                                   ws_acc + (int64_t)bh * nsplit * D, nsplit, D, d);
+  Elem<T>::store1(out + (int64_t)b * o_sb + (int64_t)h * o_sh + d, r);
 }
 
 struct AttnArgs {

@@ -169,7 +169,39 @@ class Qwen3Int8Engine:
         self.attn_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
         _lib.check('egpt_argmax_workspace', lib.egpt_argmax_workspace(c.vocab, need))
         self.arg_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
+        self._build_step_desc()
         self.graph = None
+
+    def _build_step_desc(self):
+        """The egpt_qwen3_step descriptor of the fused decode step (pointers into this engine's tensors)."""
+        c, lib = self.cfg, _lib.lib()
+        ptr = (lambda t: t.data_ptr())
+        self._layers_c = (_lib.Qwen3Layer * c.layers)()
+        for i, L in enumerate(self.layers):
+            e = self._layers_c[i]
+            e.qkv_w, e.qkv_s = ptr(L['qkv_q']), ptr(L['qkv_s'])
+            e.o_w, e.o_s = ptr(L['o_q']), ptr(L['o_s'])
+            e.gu_w, e.gu_s = ptr(L['gu_q']), ptr(L['gu_s'])
+            e.down_w, e.down_s = ptr(L['down_q']), ptr(L['down_s'])
+            e.in_norm, e.post_norm = ptr(L['in_w']), ptr(L['post_w'])
+            e.q_norm, e.k_norm = ptr(L['qn_w']), ptr(L['kn_w'])
+            e.k_cache, e.v_cache = ptr(self.k_cache[i]), ptr(self.v_cache[i])
+        d = _lib.Qwen3Step()
+        d.layers, d.hidden, d.inter = c.layers, c.hidden, c.inter
+        d.heads, d.kv_heads, d.head_dim, d.vocab = c.heads, c.kv_heads, c.head_dim, c.vocab
+        d.cap, d.nsplit, d.eps = self.cap, self.nsplit, c.rms_eps
+        d.layer = ctypes.cast(self._layers_c, ctypes.c_void_p)
+        d.embed, d.final_norm = ptr(self.embed), ptr(self.norm_w)
+        d.head_w, d.head_s = ptr(self.head_q), ptr(self.head_s)
+        d.rope_cos, d.rope_sin = ptr(self.cos), ptr(self.sin)
+        d.token, d.position = ptr(self.token), ptr(self.position)
+        d.x, d.qkv, d.attn, d.act, d.logits = ptr(self.x), ptr(self.qkv), ptr(self.attn), ptr(self.act), ptr(self.logits)
+        need = ctypes.c_size_t()
+        _lib.check('egpt_qwen3_step_workspace', lib.egpt_qwen3_step_workspace(ctypes.byref(d), ctypes.byref(need)))
+        # zeroed once: the kernels' hand-off counters start at zero and are returned to zero by the kernels
+        self.step_ws = torch.zeros(need.value, device=self.device, dtype=torch.uint8)
+        d.workspace, d.workspace_bytes = ptr(self.step_ws), need.value
+        self._step_c = d
 
     # ------------------------------------------------------------------ construction helpers
 
@@ -298,7 +330,15 @@ class Qwen3Int8Engine:
 
     @torch.inference_mode()
     def step(self):
-        """One decode step on the current stream: consumes self.token at self.position, writes the next token."""
+        """One decode step on the current stream: consumes self.token at self.position, writes the next token.
+
+        The fused step (egpt_qwen3_decode_step): five launches per layer and one for the head."""
+        _lib.check('egpt_qwen3_decode_step', _lib.lib().egpt_qwen3_decode_step(ctypes.byref(self._step_c),
+                                                                               self._stream()))
+
+    @torch.inference_mode()
+    def step_unfused(self):
+        """The same step with one kernel per op (embedding, norms, GEMVs, rope, attention, SwiGLU, argmax)."""
         lib, c = _lib.lib(), self.cfg
         _lib.check('egpt_embed', lib.egpt_embed(self.token.data_ptr(), 1, self.embed.data_ptr(), self.embed.stride(0),
                                                 c.vocab, self.x.data_ptr(), self.x.stride(0), c.hidden,

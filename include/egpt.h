@@ -137,6 +137,73 @@ int egpt_argmax_workspace(int n, size_t *bytes);
 int egpt_argmax(const void *logits, int n, void *workspace, size_t workspace_bytes, int64_t *token,
                 int64_t *position, hipStream_t stream);
 
+/*
+ * Whole batch-1 decode step of a Qwen3 decoder with int8 weight-only linears,
+ * fused into 5 launches per layer plus one for the head (RMSNorm in the GEMV
+ * prologues; residual adds and SwiGLU in the GEMV epilogues; q/k-norm, RoPE,
+ * the K/V cache write and the split-K combine inside the attention kernel; the
+ * embedding gather inside layer 0; lm_head + argmax + position advance in the
+ * last launch). Consumes *token at *position, writes K/V slot *position of every
+ * layer, leaves the greedy next token in *token and advances *position by one.
+ * Replaces the reference's captured decode step, the Inductor-compiled HF
+ * forward + argmax + token/position update (research/realmodel/fast_decode.py:45-49),
+ * with every linear on its int8 GEMV contract (research/realmodel/int8_linear.py:26-38).
+ *
+ * Weights are device pointers, row-major [rows, cols]:
+ *   qkv_w [(heads + 2 kv_heads) head_dim, hidden]  (q rows, then k, then v)
+ *   o_w   [hidden, heads head_dim]
+ *   gu_w  [2 inter, hidden]                        (gate rows, then up rows)
+ *   down_w [hidden, inter],  head_w [vocab, hidden]
+ * with fp32 per-row scales; norms bf16; caches bf16 [kv_heads, cap, head_dim];
+ * rope_cos / rope_sin bf16 [cap, head_dim]; x / qkv / attn / act / logits are
+ * bf16 rows of hidden / (heads + 2 kv_heads) head_dim / heads head_dim / inter /
+ * vocab elements (logits may be NULL). `layer` is a HOST array of `layers` entries.
+ * The workspace (egpt_qwen3_step_workspace bytes, 256-byte aligned) must be zeroed
+ * once before the first step; the kernels return its counters to zero.
+ * Sizes: hidden, inter and heads*head_dim multiples of 16 and <= 12288;
+ * head_dim in {32, 64, 128}; heads / kv_heads in {1, 2, 4, 8}.
+ */
+typedef struct egpt_qwen3_layer {
+  const int8_t *qkv_w;
+  const float *qkv_s;
+  const int8_t *o_w;
+  const float *o_s;
+  const int8_t *gu_w;
+  const float *gu_s;
+  const int8_t *down_w;
+  const float *down_s;
+  const void *in_norm;
+  const void *post_norm;
+  const void *q_norm;
+  const void *k_norm;
+  void *k_cache;
+  void *v_cache;
+} egpt_qwen3_layer;
+
+typedef struct egpt_qwen3_step {
+  int layers, hidden, inter, heads, kv_heads, head_dim, vocab, cap, nsplit;
+  float eps;
+  const egpt_qwen3_layer *layer;
+  const void *embed;
+  const void *final_norm;
+  const int8_t *head_w;
+  const float *head_s;
+  const void *rope_cos;
+  const void *rope_sin;
+  int64_t *token;
+  int64_t *position;
+  void *x;
+  void *qkv;
+  void *attn;
+  void *act;
+  void *logits;
+  void *workspace;
+  size_t workspace_bytes;
+} egpt_qwen3_step;
+
+int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
+int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,8 @@ pytestmark = pytest.mark.gpu
 
 # Qwen3-1.7B head geometry (16 q / 8 kv heads, D = 128) at a small width and depth
 SMALL = Qwen3Shape(vocab=2048, hidden=512, inter=1024, layers=3, heads=16, kv_heads=8, head_dim=128)
+# Qwen3-1.7B widths (hidden 2048, intermediate 6144, vocab 151936) at two layers
+WIDE2 = Qwen3Shape(vocab=151936, hidden=2048, inter=6144, layers=2, heads=16, kv_heads=8, head_dim=128)
 
 
 def build(shape, seed, std, cap):
@@ -95,6 +97,58 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
         agree += a
         total += n
     assert agree / total >= 0.95, agree / total
+
+
+@pytest.mark.parametrize('shape,std', [(TINY, 0.2), (SMALL, 0.15)])
+def test_fused_step_matches_unfused_step(shape, std):
+    """The fused step (5 launches per layer) against the one-kernel-per-op step on the same tokens."""
+    eng, _ = build(shape, seed=11, std=std, cap=96)
+    prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(3))
+    runs = {}
+    for name, fn in (('unfused', eng.step_unfused), ('fused', eng.step)):
+        eng.reset()
+        eng.prefill(prompt)
+        toks, logits = [], []
+        forced = runs.get('unfused', (None,))[0]
+        for i in range(12):
+            if forced is not None and i > 0:
+                eng.token.fill_(forced[i - 1])  # same inputs even past a near-tie
+            fn()
+            toks.append(int(eng.token))
+            logits.append(eng.logits[0].float().cpu().clone())
+        torch.cuda.synchronize()
+        runs[name] = (toks, logits, eng.k_cache.float().cpu().clone(), eng.v_cache.float().cpu().clone(),
+                      int(eng.position))
+    (tu, lu, ku, vu, pu), (tf, lf, kf, vf, pf) = runs['unfused'], runs['fused']
+    assert pu == pf == 9 + 12
+    for a, b in zip(lu, lf):
+        assert float((a - b).abs().max()) <= 2e-2 * float(a.abs().max())
+    assert float((ku - kf).abs().max()) <= 2e-2 * float(ku.abs().max())
+    assert torch.equal(vu[:, :, :9], vf[:, :, :9])  # prompt slots come from the same prefill
+    assert float((vu - vf).abs().max()) <= 2e-2 * float(vu.abs().max())
+    agree = sum(a == b for a, b in zip(tu, tf))
+    assert agree >= 11, (tu, tf)
+
+
+def test_qwen3_1p7b_widths_match_oracle():
+    """Real Qwen3-1.7B widths (hidden 2048, inter 6144, vocab 151936, 16/8 heads) at two layers:
+    prefill logits and teacher-forced greedy steps of the fused step against the CPU oracle."""
+    eng, orc = build(WIDE2, seed=21, std=0.05, cap=64)
+    prompt = torch.randint(0, WIDE2.vocab, (16,), generator=torch.Generator().manual_seed(5))
+    ref, margins, tops = oracle_greedy_with_margins(orc, prompt, 12)
+    assert len(set(ref)) > 4
+    a, n, bad = teacher_forced_agreement(eng, prompt, ref, margins, tops)
+    assert not bad, bad
+    assert a >= n - 1, (a, n)
+    # logits of the last teacher-forced step against the oracle's
+    orc.reset()
+    logits, pos = orc.forward(prompt, 0), len(prompt)
+    for t in ref[:-1]:
+        logits = orc.forward([t], pos)
+        pos += 1
+    got = eng.logits[0].float().cpu()
+    want = logits.float()
+    assert float((got - want).abs().max()) <= 2e-2 * float(want.abs().max())
 
 
 def test_graph_replay_equals_eager_step():
