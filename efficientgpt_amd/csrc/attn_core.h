@@ -34,18 +34,56 @@ struct AttnGeom {
   static_assert(LPS >= 1 && LPS <= 64 && (kWave % LPS) == 0, "unsupported head dim / dtype");
 };
 
+// K/V rows in flight for one softmax stream (register double buffer).
+struct AttnPipe {
+  u32x4 kr[kAttnUnroll], vr[kAttnUnroll];
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void attn_issue(AttnPipe& pp, const T* __restrict__ kb, int64_t k_sn,
+                                           const T* __restrict__ vb, int64_t v_sn, int64_t base, int64_t end) {
+  constexpr int NG = AttnGeom<T, D>::NG;
+#pragma unroll
+  for (int u = 0; u < kAttnUnroll; ++u) {
+    const int64_t n = base + (int64_t)u * NG;
+    const int64_t nn = n < end ? n : base;  // never touch slots past the live range
+    pp.kr[u] = ld16(kb + nn * k_sn);
+    pp.vr[u] = ld16(vb + nn * v_sn);
+  }
+}
+
+// Issue this thread's first K/V loads of slots [start, end); attn_partial()
+// continues from them. Splitting the two lets a caller overlap the first round
+// trip with work of its own (computing the query).
+template <typename T, int D>
+__device__ __forceinline__ void attn_begin(AttnPipe& pp, const T* __restrict__ kbase, int64_t k_sn,
+                                           const T* __restrict__ vbase, int64_t v_sn, int64_t start, int64_t end) {
+  constexpr int EPL = AttnGeom<T, D>::EPL;
+  constexpr int LPS = AttnGeom<T, D>::LPS;
+  const int tid = threadIdx.x;
+  const int d0 = (tid % LPS) * EPL;
+  const int64_t n0 = start + tid / LPS;
+  if (n0 < end) attn_issue<T, D>(pp, kbase + d0, k_sn, vbase + d0, v_sn, n0, end);
+}
+
 // One block's partial softmax state over slots [start, end) of one kv head, for
 // the G query heads of its group (qf: this thread's EPL elements of each query,
-// in fp32). Writes (m, l, acc[D]) of every query head to
+// in fp32), continuing from attn_begin(). If xk is non-null, one more slot with
+// key xk / value xv (this thread's EPL elements, fp32) is folded in by the
+// first stream of the block: the new token of a decode step, taken from
+// registers instead of being read back from the cache. Writes (m, l, acc[D])
+// of every query head to
 //   ws_m[row + g * nsplit], ws_l[...], ws_acc[(row + g * nsplit) * D + d]
-// where row = (b * Hq + hk * G) * nsplit + split. start >= end gives the empty
-// state (m = -inf, l = 0, acc = 0). Must be called by all 256 threads.
+// where row = (b * Hq + hk * G) * nsplit + split. An empty range with no extra
+// slot gives the empty state (m = -inf, l = 0, acc = 0). Must be called by all
+// 256 threads.
 template <typename T, int D, int G>
-__device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>::EPL], const T* __restrict__ kbase,
-                                             int64_t k_sn, const T* __restrict__ vbase, int64_t v_sn, int64_t start,
-                                             int64_t end, float scale, float* __restrict__ ws_m,
-                                             float* __restrict__ ws_l, float* __restrict__ ws_acc, int64_t row,
-                                             int nsplit) {
+__device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>::EPL], AttnPipe& pp,
+                                             const T* __restrict__ kbase, int64_t k_sn, const T* __restrict__ vbase,
+                                             int64_t v_sn, int64_t start, int64_t end, float scale,
+                                             float* __restrict__ ws_m, float* __restrict__ ws_l,
+                                             float* __restrict__ ws_acc, int64_t row, int nsplit,
+                                             const float* xk = nullptr, const float* xv = nullptr) {
   constexpr int EPL = AttnGeom<T, D>::EPL;
   constexpr int LPS = AttnGeom<T, D>::LPS;
   constexpr int NG = AttnGeom<T, D>::NG;
@@ -68,26 +106,14 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
   // Register double buffer: the loads of iteration i+1 are issued before the
   // arithmetic of iteration i, so each wavefront keeps 2 * kAttnUnroll K and V
   // rows in flight instead of waiting on every round trip.
-  u32x4 kr[kAttnUnroll], vr[kAttnUnroll];
-  auto issue = [&](int64_t base, u32x4* kd, u32x4* vd) {
-#pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) {
-      const int64_t n = base + (int64_t)u * NG;
-      const int64_t nn = n < end ? n : base;  // never touch slots past the live range
-      kd[u] = ld16(kbase + nn * k_sn);
-      vd[u] = ld16(vbase + nn * v_sn);
-    }
-  };
-  int64_t n0 = start + grp;
-  if (n0 < end) issue(n0, kr, vr);
-  for (; n0 < end; n0 += kStep) {
+  for (int64_t n0 = start + grp; n0 < end; n0 += kStep) {
     u32x4 kc[kAttnUnroll], vc[kAttnUnroll];
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
-      kc[u] = kr[u];
-      vc[u] = vr[u];
+      kc[u] = pp.kr[u];
+      vc[u] = pp.vr[u];
     }
-    if (n0 + kStep < end) issue(n0 + kStep, kr, vr);
+    if (n0 + kStep < end) attn_issue<T, D>(pp, kbase, k_sn, vbase, v_sn, n0 + kStep, end);
 
     float s[kAttnUnroll][G];
 #pragma unroll
@@ -130,6 +156,25 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
         acc[g][e] = a;
       }
       m[g] = mt;
+    }
+  }
+
+  if (xk) {  // block-uniform: the extra slot goes to stream 0
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float p = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], xk[e], p);
+      const float sx = group_sum<LPS>(p) * scale;
+      if (grp == 0) {
+        const float mt = fmaxf(m[g], sx);
+        const float alpha = exp2f((m[g] - mt) * kLog2e);  // 0 when the stream was empty
+        const float px = exp2f((sx - mt) * kLog2e);
+        l[g] = l[g] * alpha + px;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(px, xv[e], acc[g][e] * alpha);
+        m[g] = mt;
+      }
     }
   }
 

@@ -33,15 +33,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
   int64_t start, end;
   attn_split_range(len, nsplit, split, start, end);
 
+  u32x4 qr[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qr[g] = ld16(q + (int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d0);
+  const T* kb = k + (int64_t)b * k_sb + (int64_t)hk * k_sh;
+  const T* vb = v + (int64_t)b * v_sb + (int64_t)hk * v_sh;
+  AttnPipe pp;
+  attn_begin<T, D>(pp, kb, k_sn, vb, v_sn, start, end);
   float qf[G][EPL];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const T* qp = q + (int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d0;
-    Elem<T>::unpack(ld16(qp), qf[g]);
-  }
-  attn_partial<T, D, G>(qf, k + (int64_t)b * k_sb + (int64_t)hk * k_sh, k_sn, v + (int64_t)b * v_sb + (int64_t)hk * v_sh,
-                        v_sn, start, end, scale, ws_m, ws_l, ws_acc, ((int64_t)b * Hq + hk * G) * nsplit + split,
-                        nsplit);
+  for (int g = 0; g < G; ++g) Elem<T>::unpack(qr[g], qf[g]);
+  attn_partial<T, D, G>(qf, pp, kb, k_sn, vb, v_sn, start, end, scale, ws_m, ws_l, ws_acc,
+                        ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit);
 }
 
 // Partial-softmax reduce: one block per (b, query head), one thread per d.

@@ -1,13 +1,12 @@
-// Fused batch-1 Qwen3 decode step on gfx950 (MI355X): six launches per layer
-// instead of ten, and two for the head, so the step is bound by weight streaming
-// rather than by kernel count.
+// Fused batch-1 Qwen3 decode step on gfx950 (MI355X): five launches per layer
+// (six past 16 attention splits) instead of ten, and two for the head.
 //
 // Per layer (x is the bf16 residual stream, one row):
 //   1. qkv  = int8 GEMV( RMSNorm(x; input_layernorm) )               [norm in the GEMV prologue]
-//   2. attn = split-K GQA attention over slots 0..p of q_norm/k_norm + RoPE
-//             of qkv, which also writes K/V slot p; then a small kernel merges
-//             the partial softmax states
-//   3. x    = bf16( x + int8 GEMV(attn; o_proj) )                    [residual in the epilogue]
+//   2. split-K GQA attention partials over slots 0..p of q_norm/k_norm + RoPE
+//      of qkv, which also writes K/V slot p
+//   3. x    = bf16( x + int8 GEMV(merge(partials); o_proj) )         [merge in the prologue,
+//                                                                     residual in the epilogue]
 //   4. act  = SwiGLU( int8 GEMV( RMSNorm(x; post_attention_layernorm) ; gate|up ) )
 //   5. x    = bf16( x + int8 GEMV(act; down_proj) )
 // Head: logits = int8 GEMV( RMSNorm(x; norm) ; lm_head ) with per-block maxima,
@@ -42,6 +41,15 @@ enum { kEpiStore = 0, kEpiResid = 1, kEpiSwiGLU = 2, kEpiArgmax = 3 };
 
 __device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Workgroup barrier ordering LDS only. __syncthreads() also waits for every
+// outstanding global load of the wavefront (s_waitcnt vmcnt(0)), which would
+// stall the block behind its whole weight stream at each LDS hand-off.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 struct FusedGemv {
   const uint16_t* x;       // activation row, or a table when x_token is set
   const int64_t* x_token;  // device id selecting row x + token * x_ld (the embedding gather)
@@ -60,6 +68,11 @@ struct FusedGemv {
   int64_t resid_ld;
   float* part_v;           // Argmax: per-block maxima (value, first index)
   int* part_i;
+  const float* ws_m;       // kXMerge: split-K partials of K / head_dim heads
+  const float* ws_l;
+  const float* ws_acc;
+  int nsplit;
+  int head_dim;
 };
 
 // 16 int8 weights times 16 fp32 activations, biased form: (w + 128) converts
@@ -95,9 +108,10 @@ __device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
   return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
 }
 
+template <int W>
 __device__ __forceinline__ ArgBest block_argbest(ArgBest x) {
-  __shared__ float sv[kFWaves];
-  __shared__ int si[kFWaves];
+  __shared__ float sv[W];
+  __shared__ int si[W];
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     ArgBest o;
@@ -110,11 +124,11 @@ __device__ __forceinline__ ArgBest block_argbest(ArgBest x) {
     sv[wave] = x.v;
     si[wave] = x.i;
   }
-  __syncthreads();
+  lds_barrier();
   ArgBest r{sv[0], si[0]};
 #pragma unroll
-  for (int j = 1; j < kFWaves; ++j) r = arg_better(r, ArgBest{sv[j], si[j]});
-  __syncthreads();
+  for (int j = 1; j < W; ++j) r = arg_better(r, ArgBest{sv[j], si[j]});
+  lds_barrier();
   return r;
 }
 
@@ -126,122 +140,262 @@ __device__ __forceinline__ const uint16_t* token_row(const uint16_t* base, const
   return base + t * ld;
 }
 
+// Activation source of a fused GEMV.
+enum { kXRow = 0, kXMerge = 1 };
+
+// Largest split count the o_proj prologue merges itself: all of a thread's
+// partial loads are issued together, unrolled to this bound.
+constexpr int kMergeInGemvMaxSplits = 16;
+
+// Stage the activation row of a fused GEMV in LDS as bf16 (the value every
+// wavefront of the block multiplies), once per block:
+//   kXRow, NORM: h = bf16(w * bf16(x * rsqrt(mean x^2 + eps)))   (x from a row or table[token])
+//   kXRow:       h = x
+//   kXMerge:     h = bf16(sum_s w_s acc_s / sum_s w_s l_s), the split-K merge with
+//                attn_combine_one's arithmetic, K / head_dim heads
+// Each thread owns 8 consecutive elements per pass. The loads are issued by
+// stage_load() BEFORE the kernel's weight loads: vector loads retire in order,
+// so the activation can then be used without waiting for the weight stream.
+template <int NTHREADS>
+struct Staged {
+  static constexpr int kPasses = (kMaxChunks * kFChunk + NTHREADS * 8 - 1) / (NTHREADS * 8);
+  u32x4 xv[kPasses], nv[kPasses];
+  float mv[kMergeInGemvMaxSplits], lv[kMergeInGemvMaxSplits];
+  u32x4 lo[kMergeInGemvMaxSplits], hi[kMergeInGemvMaxSplits];
+};
+
+template <int NTHREADS, bool NORM, int XSRC>
+__device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS>& st) {
+  const int tid = threadIdx.x;
+  const u32x4 z{0u, 0u, 0u, 0u};
+  if constexpr (XSRC == kXMerge) {
+    // one pass: K <= NTHREADS * 8 is checked on the host
+    const int k8 = tid * 8;
+    const bool in_k = k8 < a.K;
+    const int D = a.head_dim;
+    const int h = in_k ? k8 / D : 0;
+    const int d = in_k ? k8 % D : 0;
+    const float* mrow = a.ws_m + (int64_t)h * a.nsplit;
+    const float* lrow = a.ws_l + (int64_t)h * a.nsplit;
+    const float* arow = a.ws_acc + (int64_t)h * a.nsplit * D + d;
+#pragma unroll
+    for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) {
+      const bool in = in_k && sp < a.nsplit;
+      st.mv[sp] = in ? mrow[sp] : -INFINITY;
+      st.lv[sp] = in ? lrow[sp] : 0.f;
+      st.lo[sp] = in ? ld16(arow + (int64_t)sp * D) : z;
+      st.hi[sp] = in ? ld16(arow + (int64_t)sp * D + 4) : z;
+    }
+  } else {
+    const uint16_t* xr = token_row(a.x, a.x_token, a.x_ld, a.x_rows);
+#pragma unroll
+    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+      const int k8 = (p * NTHREADS + tid) * 8;
+      const bool in = k8 < a.K;
+      st.xv[p] = in ? ld16(xr + k8) : z;
+      if constexpr (NORM) st.nv[p] = in ? ld16(a.norm_w + k8) : z;
+    }
+  }
+}
+
+template <int NTHREADS, bool NORM, int XSRC>
+__device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NTHREADS>& st, uint16_t* hs) {
+  const int tid = threadIdx.x;
+  if constexpr (XSRC == kXMerge) {
+    const int k8 = tid * 8;
+    if (k8 < a.K) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) mx = fmaxf(mx, st.mv[sp]);
+      float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float ls = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) {
+        if (st.mv[sp] == -INFINITY) continue;  // empty (or absent) split: weight 0
+        const float wgt = exp2f((st.mv[sp] - mx) * kLog2e);
+        const float v8[8] = {__uint_as_float(st.lo[sp].x), __uint_as_float(st.lo[sp].y),
+                             __uint_as_float(st.lo[sp].z), __uint_as_float(st.lo[sp].w),
+                             __uint_as_float(st.hi[sp].x), __uint_as_float(st.hi[sp].y),
+                             __uint_as_float(st.hi[sp].z), __uint_as_float(st.hi[sp].w)};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc8[e] = fmaf(wgt, v8[e], acc8[e]);
+        ls = fmaf(wgt, st.lv[sp], ls);
+      }
+      uint32_t pk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pk[e] = (uint32_t)f32_to_bf16(acc8[2 * e] / ls) | ((uint32_t)f32_to_bf16(acc8[2 * e + 1] / ls) << 16);
+      *(u32x4*)(hs + k8) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+  } else if constexpr (NORM) {
+    __shared__ float red[NTHREADS / kWave];
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+      float v[8];
+      Elem<__bf16>::unpack(st.xv[p], v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+    ss = wave_sum(ss);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+    lds_barrier();
+    float total = 0.f;
+#pragma unroll
+    for (int j = 0; j < NTHREADS / kWave; ++j) total += red[j];
+    const float inv = rsqrtf(total / (float)a.K + a.eps);
+#pragma unroll
+    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+      const int k8 = (p * NTHREADS + tid) * 8;
+      if (k8 < a.K) {
+        float v[8], w[8];
+        Elem<__bf16>::unpack(st.xv[p], v);
+        Elem<__bf16>::unpack(st.nv[p], w);
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pk[e] = (uint32_t)f32_to_bf16(w[2 * e] * bf16r(v[2 * e] * inv)) |
+                  ((uint32_t)f32_to_bf16(w[2 * e + 1] * bf16r(v[2 * e + 1] * inv)) << 16);
+        *(u32x4*)(hs + k8) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+      const int k8 = (p * NTHREADS + tid) * 8;
+      if (k8 < a.K) *(u32x4*)(hs + k8) = st.xv[p];
+    }
+  }
+  lds_barrier();
+}
+
+// Weight rows of wave tile t (RH output features; SwiGLU: RH gate rows then the
+// RH matching up rows) and the epilogue operands of the feature lane j < RH
+// stores. Rows past N are clamped to N - 1 and never stored.
+template <int R, int NCH, int EPI>
+struct GemvTile {
+  static constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
+  u32x4 w[NCH][R];
+  float sc, sc_up, res;
+
+  __device__ __forceinline__ void load(const FusedGemv& a, int64_t t, int lane) {
+    const int64_t f0 = t * RH;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t fr = min(f0 + (r % RH), (int64_t)a.N - 1);
+      const int8_t* row = a.w + ((EPI == kEpiSwiGLU && r >= RH) ? fr + a.N : fr) * a.ldw;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int k = c * kFChunk + lane * 16;
+        w[c][r] = k < a.K ? ld16_stream(row + k) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    const int64_t fc = min(f0 + (lane < RH ? lane : 0), (int64_t)a.N - 1);
+    sc = a.scale[fc];
+    sc_up = EPI == kEpiSwiGLU ? a.scale[a.N + fc] : 0.f;
+    res = EPI == kEpiResid ? bf16_to_f32(token_row(a.resid, a.resid_token, a.resid_ld, a.x_rows)[fc]) : 0.f;
+  }
+};
+
 // One int8 GEMV of a single activation row with a fused prologue / epilogue.
-// A block is 4 wavefronts; a wavefront owns RH output features (R weight rows:
-// SwiGLU pairs each gate row with its up row) and streams them with 16-byte
-// loads, all NCH chunks of all R rows issued before any arithmetic. With NORM,
-// each wavefront reduces mean(x^2) over its own copy of the row (every lane
-// holds 16 * NCH elements, which together tile the row once).
-template <int R, int NCH, int EPI, bool NORM>
-__global__ __launch_bounds__(kFThreads) void fused_gemv_kernel(const FusedGemv a) {
-  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
+// A block is W wavefronts. A wavefront owns RH output features per tile (R
+// weight rows: SwiGLU pairs each gate row with its up row) and walks tiles
+// t, t + stride, ... (one tile per wavefront unless the grid is capped, as for
+// the lm_head), streaming each tile's rows with 16-byte non-temporal loads and
+// prefetching the next tile's rows while it multiplies the current one. The
+// activation is staged once per block in LDS (stage_activation), its loads
+// issued before the weights: vector loads retire in order. LDS hand-offs use
+// lds_barrier(), which does not wait for the weight stream. Argmax: each lane
+// keeps its best (value, index) across tiles; the block reduces once.
+template <int R, int NCH, int EPI, bool NORM, int XSRC, int W>
+__global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a) {
+  using Tile = GemvTile<R, NCH, EPI>;
+  constexpr int RH = Tile::RH;
   static_assert(EPI != kEpiSwiGLU || R % 2 == 0, "SwiGLU pairs rows");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int64_t f0 = ((int64_t)blockIdx.x * kFWaves + wave) * RH;
-  const bool active = f0 < a.N;
+  const int64_t ntiles = (a.N + RH - 1) / RH;
+  const int64_t stride = (int64_t)gridDim.x * W;
+  int64_t t = (int64_t)blockIdx.x * W + wave;
 
-  const int8_t* wrow[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t f = min(f0 + (r % RH), (int64_t)a.N - 1);
-    wrow[r] = a.w + ((EPI == kEpiSwiGLU && r >= RH) ? f + a.N : f) * a.ldw;
-  }
-  // Weights first: they do not depend on the activation.
-  u32x4 wv[NCH][R];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int k = c * kFChunk + lane * 16;
-    const bool kin = k < a.K;
-#pragma unroll
-    for (int r = 0; r < R; ++r) wv[c][r] = kin ? ld16_stream(wrow[r] + k) : u32x4{0u, 0u, 0u, 0u};
-  }
+  // Activation loads first (they retire first), then the weight stream.
+  Staged<W * kWave> stg;
+  stage_load<W * kWave, NORM, XSRC>(a, stg);
+  Tile cur;
+  cur.load(a, t, lane);
+  __shared__ __align__(16) uint16_t hs[NCH * kFChunk];
+  stage_finish<W * kWave, NORM, XSRC>(a, stg, hs);
 
-  const uint16_t* xr = token_row(a.x, a.x_token, a.x_ld, a.x_rows);
-  float xf[NCH][16];
+  // Only the capped lm_head grid walks several tiles per wavefront; the other
+  // launches give every wavefront one tile, so they keep no second buffer.
+  constexpr bool kMulti = EPI == kEpiArgmax;
+  ArgBest best{-INFINITY, 0x7fffffff};
+  for (; t < ntiles; t += stride) {
+    const bool more = kMulti && t + stride < ntiles;
+    Tile nxt;
+    if (more) nxt.load(a, t + stride, lane);
+
+    float acc[R];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int k = c * kFChunk + lane * 16;
-    if (k < a.K) {
-      unpack_bf16x16(ld16(xr + k), ld16(xr + k + 8), xf[c]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) xf[c][e] = 0.f;
-    }
-  }
-  if constexpr (NORM) {
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ss = fmaf(xf[c][e], xf[c][e], ss);
-    const float inv = rsqrtf(wave_sum(ss) / (float)a.K + a.eps);
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    float sx = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int k = c * kFChunk + lane * 16;
+      float xf[16];
       if (k < a.K) {
-        float nw[16];
-        unpack_bf16x16(ld16(a.norm_w + k), ld16(a.norm_w + k + 8), nw);
+        unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
+      } else {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) xf[c][e] = bf16r(nw[e] * bf16r(xf[c][e] * inv));
+        for (int e = 0; e < 16; ++e) xf[e] = 0.f;
+      }
+      float ts = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ts += xf[e];
+      sx += ts;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xf, acc[r]);
+    }
+
+    // Row totals (wave-uniform); lane j < RH keeps feature t * RH + j.
+    float mine = 0.f, mine_up = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[r] - 128.f * sx);
+      if (r < RH) {
+        if (lane == r) mine = v;
+      } else {
+        if (lane == r - RH) mine_up = v;
       }
     }
-  }
-
-  float acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  float sx = 0.f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    float t = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) t += xf[c][e];
-    sx += t;
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = dot16_biased(wv[c][r], xf[c], acc[r]);
-  }
-
-  // Row totals (wave-uniform); lane j < RH keeps feature f0 + j.
-  float mine = 0.f, mine_up = 0.f;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float v = wave_sum(acc[r] - 128.f * sx);
-    if (r < RH) {
-      if (lane == r) mine = v;
+    const int64_t f = t * RH + lane;
+    const bool own = lane < RH && f < a.N;
+    if constexpr (EPI == kEpiStore) {
+      if (own) a.y[f] = f32_to_bf16(mine * cur.sc);
+    } else if constexpr (EPI == kEpiResid) {
+      if (own) a.y[f] = f32_to_bf16(cur.res + bf16r(mine * cur.sc));
+    } else if constexpr (EPI == kEpiSwiGLU) {
+      if (own) {
+        const float g = bf16r(mine * cur.sc);
+        const float u = bf16r(mine_up * cur.sc_up);
+        const float sg = bf16r(g / (1.0f + expf(-g)));
+        a.y[f] = f32_to_bf16(sg * u);
+      }
     } else {
-      if (lane == r - RH) mine_up = v;
+      if (own) {
+        const uint16_t lg = f32_to_bf16(mine * cur.sc);
+        if (a.y) a.y[f] = lg;
+        best = arg_better(best, ArgBest{bf16_to_f32(lg), (int)f});
+      }
     }
+    if (more) cur = nxt;
   }
-  const int64_t f = f0 + lane;
-  const bool own = active && lane < RH && f < a.N;
 
-  if constexpr (EPI == kEpiStore) {
-    if (own) a.y[f] = f32_to_bf16(mine * a.scale[f]);
-  } else if constexpr (EPI == kEpiResid) {
-    if (own) {
-      const float o = bf16r(mine * a.scale[f]);
-      const uint16_t* rr = token_row(a.resid, a.resid_token, a.resid_ld, a.x_rows);
-      a.y[f] = f32_to_bf16(bf16_to_f32(rr[f]) + o);
-    }
-  } else if constexpr (EPI == kEpiSwiGLU) {
-    if (own) {
-      const float g = bf16r(mine * a.scale[f]);
-      const float u = bf16r(mine_up * a.scale[a.N + f]);
-      const float sg = bf16r(g / (1.0f + expf(-g)));
-      a.y[f] = f32_to_bf16(sg * u);
-    }
-  } else {  // per-block maximum of the logits
-    ArgBest b{-INFINITY, 0x7fffffff};
-    if (own) {
-      const uint16_t lg = f32_to_bf16(mine * a.scale[f]);
-      if (a.y) a.y[f] = lg;
-      b = ArgBest{bf16_to_f32(lg), (int)f};
-    }
-    b = block_argbest(b);
+  if constexpr (EPI == kEpiArgmax) {  // per-block maximum of the logits
+    best = block_argbest<W>(best);
     if (threadIdx.x == 0) {
-      a.part_v[blockIdx.x] = b.v;
-      a.part_i[blockIdx.x] = b.i;
+      a.part_v[blockIdx.x] = best.v;
+      a.part_i[blockIdx.x] = best.i;
     }
   }
 }
@@ -254,7 +408,7 @@ __global__ __launch_bounds__(kFThreads) void argmax_final_kernel(const float* __
                                                                  int64_t* __restrict__ position) {
   ArgBest best{-INFINITY, 0x7fffffff};
   for (int j = threadIdx.x; j < parts; j += kFThreads) best = arg_better(best, ArgBest{part_v[j], part_i[j]});
-  best = block_argbest(best);
+  best = block_argbest<kFWaves>(best);
   if (threadIdx.x == 0) {
     *token = best.i == 0x7fffffff ? 0 : best.i;  // all-NaN logits: token 0
     *position += 1;
@@ -279,16 +433,17 @@ struct AttnStep {
 };
 
 // Head-wise RMSNorm + RoPE of one head held by an LPS-lane group (EPL elements
-// per lane, element d0 + e). rotate_half pairs element i with i +- D/2, which
-// sits in lane (sub ^ LPS/2) at the same e.
+// per lane, element d0 + e; x, norm weight, cos and sin rows already loaded).
+// rotate_half pairs element i with i +- D/2, which sits in lane (sub ^ LPS/2)
+// at the same e.
 template <int D, int EPL, int LPS>
-__device__ __forceinline__ void head_norm_rope(const uint16_t* src, const uint16_t* nw, const uint16_t* cr,
-                                               const uint16_t* sr, int d0, float eps, float (&out)[EPL]) {
+__device__ __forceinline__ void head_norm_rope(const u32x4 xr, const u32x4 wr, const u32x4 cr, const u32x4 sr, int d0,
+                                               float eps, float (&out)[EPL]) {
   float xv[EPL], w[EPL], cs[EPL], sn[EPL];
-  Elem<__bf16>::unpack(ld16(src + d0), xv);
-  Elem<__bf16>::unpack(ld16(nw + d0), w);
-  Elem<__bf16>::unpack(ld16(cr + d0), cs);
-  Elem<__bf16>::unpack(ld16(sr + d0), sn);
+  Elem<__bf16>::unpack(xr, xv);
+  Elem<__bf16>::unpack(wr, w);
+  Elem<__bf16>::unpack(cr, cs);
+  Elem<__bf16>::unpack(sr, sn);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) ss = fmaf(xv[e], xv[e], ss);
@@ -305,10 +460,13 @@ __device__ __forceinline__ void head_norm_rope(const uint16_t* src, const uint16
   }
 }
 
-// Attention partials of one decode step: block (kv head, split). Query and new
-// key are normalised and rotated in the prologue (each block redoes its G query
-// heads: 2 x 128 elements); the block whose split holds slot p writes the new K
-// and V rows there before reading its range, and no other block touches slot p.
+// Attention partials of one decode step: block (kv head, split). Every load
+// that does not depend on arithmetic is issued first (queries, new key and
+// value, norm weights, RoPE rows, the first K/V rows of the split); the query
+// and the new key are normalised and rotated while those are in flight. The
+// block whose split holds slot p folds the new token in from registers (it is
+// not read back from the cache) and stores it to slot p for later steps; no
+// other block of the launch touches slot p, so no barrier orders the store.
 template <int D, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep a) {
   constexpr int EPL = AttnGeom<__bf16, D>::EPL;
@@ -324,33 +482,44 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
   const int64_t len = pos + 1;
   int64_t start, end;
   attn_split_range(len, a.nsplit, split, start, end);
-  const int64_t chunk = (len + a.nsplit - 1) / a.nsplit;
-  const bool owner = split == (int)((len - 1) / chunk);
+  const bool owner = start <= pos && pos < end;  // block-uniform
+  const int64_t end_cached = owner ? pos : end;   // slot p comes from registers
 
-  const uint16_t* cr = a.cos_t + pos * D;
-  const uint16_t* sr = a.sin_t + pos * D;
-  float qf[G][EPL];
+  u32x4 qr[G], qw, kw, kr, vr, cr, sr;
 #pragma unroll
-  for (int g = 0; g < G; ++g) head_norm_rope<D, EPL, LPS>(a.qkv + (int64_t)(hk * G + g) * D, a.q_norm_w, cr, sr, d0, a.eps, qf[g]);
+  for (int g = 0; g < G; ++g) qr[g] = ld16(a.qkv + (int64_t)(hk * G + g) * D + d0);
+  qw = ld16(a.q_norm_w + d0);
+  kw = ld16(a.k_norm_w + d0);
+  kr = ld16(a.qkv + (int64_t)(Hq + hk) * D + d0);
+  vr = ld16(a.qkv + (int64_t)(Hq + a.Hkv + hk) * D + d0);
+  cr = ld16(a.cos_t + pos * D + d0);
+  sr = ld16(a.sin_t + pos * D + d0);
 
   uint16_t* kc = a.k_cache + (int64_t)hk * a.c_sh;
   uint16_t* vc = a.v_cache + (int64_t)hk * a.c_sh;
-  if (owner) {  // block-uniform
-    float kn[EPL];
-    head_norm_rope<D, EPL, LPS>(a.qkv + (int64_t)(Hq + hk) * D, a.k_norm_w, cr, sr, d0, a.eps, kn);
+  AttnPipe pp;
+  attn_begin<__bf16, D>(pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached);
+
+  float qf[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) head_norm_rope<D, EPL, LPS>(qr[g], qw, cr, sr, d0, a.eps, qf[g]);
+  float kn[EPL], vn[EPL];
+  if (owner) {
+    head_norm_rope<D, EPL, LPS>(kr, kw, cr, sr, d0, a.eps, kn);
+    Elem<__bf16>::unpack(vr, vn);
     if (tid < LPS) {
       uint32_t packed[EPL / 2];
 #pragma unroll
       for (int e = 0; e < EPL / 2; ++e)
         packed[e] = (uint32_t)f32_to_bf16(kn[2 * e]) | ((uint32_t)f32_to_bf16(kn[2 * e + 1]) << 16);
       *(u32x4*)(kc + pos * a.c_sn + d0) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-      *(u32x4*)(vc + pos * a.c_sn + d0) = ld16(a.qkv + (int64_t)(Hq + a.Hkv + hk) * D + d0);
+      *(u32x4*)(vc + pos * a.c_sn + d0) = vr;
     }
-    __syncthreads();
   }
 
-  attn_partial<__bf16, D, G>(qf, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end, a.scale, a.ws_m,
-                             a.ws_l, a.ws_acc, (int64_t)(hk * G) * a.nsplit + split, a.nsplit);
+  attn_partial<__bf16, D, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
+                             a.scale, a.ws_m, a.ws_l, a.ws_acc, (int64_t)(hk * G) * a.nsplit + split, a.nsplit,
+                             owner ? kn : nullptr, owner ? vn : nullptr);
 }
 
 // Merge of the split partials: one block per query head, one thread per element.
@@ -374,20 +543,26 @@ int chunks_for(int K) {
   return 12;
 }
 
-// Output features per wavefront: the largest of 4 / 2 / 1 that still gives the
-// 256 CUs at least 256 blocks.
+// Launch shape, from a cold sweep of the Qwen3 shapes on the MI355X: 8
+// wavefronts per block (the activation row is staged once per block), two rows
+// per wavefront while that still leaves >= 256 blocks (fused QKV, lm_head;
+// gate/up as one gate + one up row), else one (o_proj, down_proj): these small
+// GEMVs are bound by latency, and more blocks start streaming sooner.
+constexpr int kGemvWaves = 8;
+
 int features_per_wave(int64_t n, bool pairs) {
-  const int hi = pairs ? 2 : 4;
-  for (int rh = hi; rh > 1; rh /= 2)
-    if ((n + (int64_t)kFWaves * rh - 1) / ((int64_t)kFWaves * rh) >= 256) return rh;
-  return 1;
+  if (pairs) return 1;  // one gate row + one up row
+  return (n + 2 * kGemvWaves - 1) / (2 * kGemvWaves) >= 256 ? 2 : 1;
 }
 
-template <int EPI, bool NORM, int R>
+template <int EPI, bool NORM, int XSRC, int R>
 int launch_r(const FusedGemv& a, int nch, unsigned blocks, hipStream_t st) {
+  constexpr int W = kGemvWaves;
   switch (nch) {
-#define EGPT_CASE(C) \
-  case C: hipLaunchKernelGGL((fused_gemv_kernel<R, C, EPI, NORM>), dim3(blocks), dim3(kFThreads), 0, st, a); break;
+#define EGPT_CASE(C)                                                                                          \
+  case C:                                                                                                     \
+    hipLaunchKernelGGL((fused_gemv_kernel<R, C, EPI, NORM, XSRC, W>), dim3(blocks), dim3(W * kWave), 0, st, a); \
+    break;
     EGPT_CASE(1) EGPT_CASE(2) EGPT_CASE(3) EGPT_CASE(4) EGPT_CASE(6) EGPT_CASE(8) EGPT_CASE(12)
 #undef EGPT_CASE
     default: return EGPT_ERR_UNSUPPORTED;
@@ -395,25 +570,33 @@ int launch_r(const FusedGemv& a, int nch, unsigned blocks, hipStream_t st) {
   return EGPT_LAUNCH_STATUS();
 }
 
-template <int EPI, bool NORM>
+// Blocks of a fused GEMV launch: one tile per wavefront, except the lm_head,
+// whose grid is capped (about four 8-wave blocks per CU) so each block stages
+// the activation once and reduces its argmax once over many tiles.
+constexpr unsigned kHeadMaxBlocks = 1024;
+
+unsigned gemv_blocks(int64_t n, bool pairs, bool capped) {
+  const int rh = features_per_wave(n, pairs);
+  const int64_t tiles = (n + rh - 1) / rh;
+  const unsigned b = (unsigned)((tiles + kGemvWaves - 1) / kGemvWaves);
+  return capped && b > kHeadMaxBlocks ? kHeadMaxBlocks : b;
+}
+
+template <int EPI, bool NORM, int XSRC = kXRow>
 int launch_fused(const FusedGemv& a, hipStream_t st) {
   const bool pairs = EPI == kEpiSwiGLU;
   const int rh = features_per_wave(a.N, pairs);
-  const unsigned blocks = (unsigned)((a.N + (int64_t)kFWaves * rh - 1) / ((int64_t)kFWaves * rh));
+  const unsigned blocks = gemv_blocks(a.N, pairs, EPI == kEpiArgmax);
   const int nch = chunks_for(a.K);
   if constexpr (EPI == kEpiSwiGLU) {
-    return rh >= 2 ? launch_r<EPI, NORM, 4>(a, nch, blocks, st) : launch_r<EPI, NORM, 2>(a, nch, blocks, st);
+    return launch_r<EPI, NORM, XSRC, 2>(a, nch, blocks, st);
   } else {
-    if (rh >= 4) return launch_r<EPI, NORM, 4>(a, nch, blocks, st);
-    if (rh >= 2) return launch_r<EPI, NORM, 2>(a, nch, blocks, st);
-    return launch_r<EPI, NORM, 1>(a, nch, blocks, st);
+    if (rh >= 2) return launch_r<EPI, NORM, XSRC, 2>(a, nch, blocks, st);
+    return launch_r<EPI, NORM, XSRC, 1>(a, nch, blocks, st);
   }
 }
 
-unsigned head_blocks(int vocab) {
-  const int rh = features_per_wave(vocab, false);
-  return (unsigned)((vocab + (int64_t)kFWaves * rh - 1) / ((int64_t)kFWaves * rh));
-}
+unsigned head_blocks(int vocab) { return gemv_blocks(vocab, false, true); }
 
 struct StepLayout {
   size_t ml, acc, part_v, part_i, total;
@@ -463,7 +646,7 @@ int check_step(const egpt_qwen3_step* s) {
 }
 
 template <int D>
-int launch_attn_step(const AttnStep& a, int G, uint16_t* out, hipStream_t st) {
+int launch_attn_step(const AttnStep& a, int G, uint16_t* out, bool merge, hipStream_t st) {
   dim3 grid((unsigned)a.Hkv, (unsigned)a.nsplit);
   switch (G) {
     case 1: hipLaunchKernelGGL((attn_step_kernel<D, 1>), grid, dim3(kAttnThreads), 0, st, a); break;
@@ -473,8 +656,9 @@ int launch_attn_step(const AttnStep& a, int G, uint16_t* out, hipStream_t st) {
     default: return EGPT_ERR_UNSUPPORTED;
   }
   if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
-  hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((unsigned)(a.Hkv * G)), dim3(D), 0, st, a.ws_m, a.ws_l, a.ws_acc,
-                     out, a.nsplit);
+  if (merge)
+    hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((unsigned)(a.Hkv * G)), dim3(D), 0, st, a.ws_m, a.ws_l,
+                       a.ws_acc, out, a.nsplit);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -544,9 +728,13 @@ extern "C" int egpt_qwen3_decode_step(const egpt_qwen3_step* s, hipStream_t stre
     at.eps = s->eps;
     at.scale = 1.0f / sqrtf((float)D);
     uint16_t* attn_out = (uint16_t*)s->attn;
-    if (D == 128) st = launch_attn_step<128>(at, G, attn_out, stream);
-    else if (D == 64) st = launch_attn_step<64>(at, G, attn_out, stream);
-    else st = launch_attn_step<32>(at, G, attn_out, stream);
+    // the o_proj prologue merges the splits itself while each thread owns one
+    // 8-element group of the attention row (heads * head_dim <= 8 per thread)
+    const bool merge_in_gemv =
+        s->nsplit <= kMergeInGemvMaxSplits && s->heads * D <= kGemvWaves * kWave * 8;
+    if (D == 128) st = launch_attn_step<128>(at, G, attn_out, !merge_in_gemv, stream);
+    else if (D == 64) st = launch_attn_step<64>(at, G, attn_out, !merge_in_gemv, stream);
+    else st = launch_attn_step<32>(at, G, attn_out, !merge_in_gemv, stream);
     if (st != EGPT_OK) return st;
     // 3. o_proj + residual (layer 0: the residual is the embedding row)
     FusedGemv o{};
@@ -561,7 +749,13 @@ extern "C" int egpt_qwen3_decode_step(const egpt_qwen3_step* s, hipStream_t stre
     o.resid = first ? (const uint16_t*)s->embed : x;
     o.resid_token = first ? s->token : nullptr;
     o.resid_ld = s->hidden;
-    if ((st = launch_fused<kEpiResid, false>(o, stream)) != EGPT_OK) return st;
+    o.ws_m = ws_m;
+    o.ws_l = ws_l;
+    o.ws_acc = ws_acc;
+    o.nsplit = s->nsplit;
+    o.head_dim = D;
+    st = merge_in_gemv ? launch_fused<kEpiResid, false, kXMerge>(o, stream) : launch_fused<kEpiResid, false>(o, stream);
+    if (st != EGPT_OK) return st;
     // 4. RMSNorm + gate/up + SwiGLU
     FusedGemv gu{};
     gu.x = x;
