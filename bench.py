@@ -1,23 +1,33 @@
 """Batch-1 int8 decode benchmark on one MI355X.
 
-Workload: a random-init Qwen3-1.7B-architecture model (28 layers, hidden 2048,
-intermediate 6144, 16 q / 8 kv heads, head_dim 128, vocab 151936, tied
-embeddings, RoPE theta 1e6), every linear int8 weight-only with per-output-channel
-scales, weights N(0, 0.02); a 128-token uniform-random prompt is prefilled, then
-each step is one replay of the captured decode graph (embedding through argmax and
-the token / position update) producing one token. Weights, cache and prompt are
-resident in HBM before timing starts.
+Workload (default): a random-init Qwen3-1.7B-architecture model (28 layers,
+hidden 2048, intermediate 6144, 16 q / 8 kv heads, head_dim 128, vocab 151936,
+tied embeddings, RoPE theta 1e6), every linear int8 weight-only with
+per-output-channel scales, weights N(0, 0.02); a 128-token uniform-random prompt
+is prefilled, then each step is one replay of the captured decode graph
+(embedding through argmax and the token / position update) producing one token.
+`--model qwen3-8b --prompt 8192` runs the long-context 8B workload instead.
+Weights, cache and prompt are resident in HBM before timing starts.
 
 Prints one JSON line:
-  value        decode tokens/s over the timed steps (GPU-side, back-to-back replays)
-  roofline     the int8 GEMV launches of one step (the dominant kernel), timed as a
-               group with HIP events on their stream: algorithmic bytes / time vs the
-               8 TB/s HBM peak
-  cpu_baseline the CPU oracle (oracle/qwen3.py, torch on the host) on a bounded sample:
-               prefill of the same prompt, then a few greedy decode steps
+  value           decode tokens/s over the timed steps (back-to-back graph replays)
+  roofline        the dominant kernel, the fused int8 GEMV (fused_gemv_kernel): the
+                  step's own GEMV launches (egpt_qwen3_step_gemvs, 4 per layer + the
+                  lm_head) replayed as one graph through egpt_int8_gemv_fused and timed
+                  with HIP events on their stream; algorithmic bytes (int8 weights +
+                  fp32 scales + bf16 activation in / out) over the average launch time.
+                  The set streams > 1.7 GB per pass, so it is HBM-cold by construction.
+  attention       split-K decode attention at the largest context of the workload
+                  family (16 q / 8 kv heads, D 128, L = 32768), rotating > 512 MB of K/V
+  step            the whole step: weight + scale + KV bytes per token / ms per token
+  copy_gbps       a device-to-device copy of 1 GiB, the measured bandwidth ceiling
+  cpu_baseline    the CPU oracle (oracle/qwen3.py, torch on the host) on a bounded
+                  sample of the same workload: prefill of the same prompt, then a few
+                  greedy decode steps, on the same weights
 """
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -29,7 +39,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-HBM_PEAK_GBPS = 8000.0
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 
 
 def parse():
@@ -42,63 +52,116 @@ def parse():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--cpu-tokens', type=int, default=8, help='decode steps in the CPU baseline sample (0: skip)')
     ap.add_argument('--no-stream', action='store_true', help='skip the streamed generate() measurement')
+    ap.add_argument('--no-extra', action='store_true', help='skip the attention and copy measurements')
     return ap.parse_args()
 
 
-def gemv_roofline(eng, reps=20):
-    """Time the int8 GEMV launches of one decode step (same shapes and buffers) as a captured graph."""
-    from efficientgpt_amd import _lib
-    lib = _lib.lib()
-    c = eng.cfg
-    calls = []
-    nbytes = 0
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def add(x, q, s, y):
-        nonlocal nbytes
-        n, k = q.shape
-        nbytes += n * k + 4 * n + 2 * k + 2 * n
-        calls.append((x, q, s, y))
 
-    for L in eng.layers:
-        add(eng.h, L['qkv_q'], L['qkv_s'], eng.qkv)
-        add(eng.attn, L['o_q'], L['o_s'], eng.o)
-        add(eng.h, L['gu_q'], L['gu_s'], eng.gu)
-        add(eng.act, L['down_q'], L['down_s'], eng.down)
-    add(eng.h, eng.head_q, eng.head_s, eng.logits)
-
-    def run():
-        st = _lib.stream_ptr(eng.device)
-        for x, q, s, y in calls:
-            _lib.check('egpt_int8_gemv', lib.egpt_int8_gemv(x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0),
-                                                            s.data_ptr(), y.data_ptr(), y.stride(0), 1, q.shape[0],
-                                                            q.shape[1], st))
-
+def _time_graph(fn, reps):
+    """Capture fn() (launches on the current stream) as one graph; mean seconds per replay."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        run()
+        fn()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        run()
+        fn()
     g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
+    e0, e1 = _events()
+    e0.record()  # on the current stream, the one the graph replays on
     for _ in range(reps):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    per_step_s = e0.elapsed_time(e1) / 1e3 / reps
-    launches = len(calls)
-    achieved = nbytes / per_step_s / 1e9
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def gemv_roofline(eng, reps=20):
+    """The step's fused GEMV launches, replayed through the public entry point, as one graph."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    n = ctypes.c_int()
+    _lib.check('egpt_qwen3_step_gemvs', lib.egpt_qwen3_step_gemvs(ctypes.byref(eng._step_c), None, 0, ctypes.byref(n)))
+    descs = (_lib.GemvFused * n.value)()
+    _lib.check('egpt_qwen3_step_gemvs', lib.egpt_qwen3_step_gemvs(ctypes.byref(eng._step_c), descs, n.value,
+                                                                  ctypes.byref(n)))
+    nbytes = sum(d.algorithmic_bytes() for d in descs)
+    head = descs[n.value - 1]
+
+    def run():
+        st = _lib.stream_ptr()
+        for d in descs:
+            _lib.check('egpt_int8_gemv_fused', lib.egpt_int8_gemv_fused(ctypes.byref(d), st))
+
+    per_pass = _time_graph(run, reps)
+    achieved = nbytes / per_pass / 1e9
     return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
             'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
-            'kernel': 'egpt int8 GEMV (gemv_i8_rows), all launches of one decode step',
-            'launches': launches, 'bytes_per_step': nbytes,
-            'avg_launch_us': round(per_step_s / launches * 1e6, 3),
-            'gemv_ms_per_step': round(per_step_s * 1e3, 4)}
+            'kernel': 'fused_gemv_kernel (int8 GEMV, RMSNorm / residual / SwiGLU / argmax fused), '
+                      'the decode step\'s own launches',
+            'launches': n.value, 'bytes_per_launch': round(nbytes / n.value),
+            'bytes_per_step': nbytes, 'avg_launch_us': round(per_pass / n.value * 1e6, 3),
+            'gemv_ms_per_step': round(per_pass * 1e3, 4),
+            'units': f'{4 * eng.cfg.layers} layer GEMVs (QKV {head.K}x{(eng.cfg.heads + 2 * eng.cfg.kv_heads) * eng.cfg.head_dim}, '
+                     f'o_proj, gate/up, down) + lm_head {head.N}x{head.K}'}
+
+
+def attention_roofline(L=32768, hq=16, hkv=8, d=128, copies=4, reps=5):
+    """Split-K GQA decode attention over all L slots, rotating `copies` K/V sets (> 512 MB)."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device('cuda')
+    g = torch.Generator(device=dev).manual_seed(7)
+    ks = [torch.randn(1, hkv, L, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    vs = [torch.randn(1, hkv, L, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    q = torch.randn(1, hq, 1, d, generator=g, device=dev).to(torch.bfloat16)
+    pos = torch.tensor([L - 1], device=dev)
+    out = torch.empty_like(q)
+    nsplit = lib.egpt_decode_attn_default_splits(1, hkv, L)
+    need = ctypes.c_size_t()
+    _lib.check('ws', lib.egpt_decode_attn_workspace(1, hq, hkv, L, d, nsplit, ctypes.byref(need)))
+    ws = torch.empty(need.value, device=dev, dtype=torch.uint8)
+
+    def run():
+        st = _lib.stream_ptr()
+        for k, v in zip(ks, vs):
+            _lib.check('egpt_decode_attn', lib.egpt_decode_attn(
+                _lib.EGPT_BF16, q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+                k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), pos.data_ptr(), 0, out.data_ptr(),
+                out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(), 1, hq, hkv, L, d, nsplit, d ** -0.5, st))
+
+    per_call = _time_graph(run, reps) / copies
+    nbytes = 2 * hkv * L * d * 2 + 2 * (2 * hq * d)
+    achieved = nbytes / per_call / 1e9
+    del ks, vs
+    torch.cuda.empty_cache()
+    return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+            'frac': round(achieved / HBM_PEAK_GBPS, 4), 'L': L, 'nsplit': nsplit,
+            'bytes_per_call': nbytes, 'us_per_call': round(per_call * 1e6, 2),
+            'kernel': 'attn_split_kernel + attn_combine_kernel (egpt_decode_attn), cold'}
+
+
+def copy_bandwidth(nbytes=1 << 30, reps=10):
+    src = torch.empty(nbytes, dtype=torch.uint8, device='cuda')
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) / 1e3 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return round(2 * nbytes / s / 1e9, 1)  # bytes read + bytes written
 
 
 def host_threads():
@@ -132,9 +195,9 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
     agree = sum(a == b for a, b in zip(toks, gpu_tokens[:n_tokens]))
     return {'value': round(decode_tps, 3) if decode_tps else None, 'unit': 'tok/s', 'cores': torch.get_num_threads(),
             'kind': 'port',
-            'sample': (f'CPU oracle (torch, bf16 activations, fp32 image of the int8 weights) on the same weights: '
-                       f'prefill of the {len(prompt)}-token prompt ({t_first - t0:.1f} s) then {n_tokens} greedy '
-                       f'tokens; decode tok/s = (n-1)/(decode time)'),
+            'sample': (f'CPU oracle (torch, bf16 activations, exact fp32 image of the int8 weights) on the same '
+                       f'weights: prefill of the {len(prompt)}-token prompt ({t_first - t0:.1f} s), then '
+                       f'{n_tokens} greedy tokens; decode tok/s = (n-1)/(decode time)'),
             'cpu': platform.processor() or platform.machine(),
             'token_agreement_with_gpu': f'{agree}/{n_tokens}'}
 
@@ -142,8 +205,8 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({'error': 'this build runs on one GPU; multi-GPU runs are not part of it',
-                          'n_gpus': args.gpus}))
+        print(json.dumps({'error': 'this build measures one GPU; runs on several GPUs are not part of it',
+                          'n_gpus': args.gpus}), flush=True)
         sys.exit(2)
     from efficientgpt_amd.fast_decode import GraphGreedyDecoder
     from efficientgpt_amd.qwen3 import QWEN3_1_7B, QWEN3_8B, Qwen3Int8Engine
@@ -151,7 +214,7 @@ def main():
     cfg = QWEN3_1_7B if args.model == 'qwen3-1.7b' else QWEN3_8B
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
-    n_stream = 256
+    n_stream = 256 if args.model == 'qwen3-1.7b' else 64
     cap = args.prompt + max(args.warmup + args.steps, n_stream) + 8
     t = time.perf_counter()
     eng = Qwen3Int8Engine.random(cfg, cap, seed=args.seed, device=dev)
@@ -162,13 +225,15 @@ def main():
     with torch.inference_mode():
         # GPU decode: prefill, capture, warm-up replays, then K timed replays back to back
         eng.reset()
+        t = time.perf_counter()
         eng.prefill(prompt)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t
         eng.capture()
-        tokens = [int(eng.token)]
         for _ in range(args.warmup):
             eng.replay()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0, e1 = _events()
         t0 = time.perf_counter()
         e0.record()
         for _ in range(args.steps):
@@ -178,6 +243,7 @@ def main():
         wall = time.perf_counter() - t0
         gpu_s = e0.elapsed_time(e1) / 1e3
         value = args.steps / wall
+        mean_len = args.prompt + args.warmup + (args.steps + 1) / 2
 
         roof = gemv_roofline(eng)
 
@@ -190,23 +256,37 @@ def main():
             stream = {'decode_tok_s': round((st['tokens'] - 1) / (st['total_s'] - st['ttft_s']), 2),
                       'ttft_ms': round(st['ttft_s'] * 1e3, 2), 'tokens': st['tokens'],
                       'distinct_tokens': len(set(out))}
-    cpu = cpu_baseline(eng, prompt, args.cpu_tokens, gpu_tokens) if args.cpu_tokens > 0 and gpu_tokens else None
+    extra = {}
+    if not args.no_extra:
+        with torch.inference_mode():  # graph capture after the engine's inference-mode captures
+            extra['attention'] = attention_roofline()
+            extra['copy_gbps'] = copy_bandwidth()
+    cpu = None
+    if args.cpu_tokens > 0 and gpu_tokens and args.model == 'qwen3-1.7b':
+        cpu = cpu_baseline(eng, prompt, args.cpu_tokens, gpu_tokens)
 
     wbytes, sbytes = cfg.weight_bytes()
+    step_bytes = wbytes + sbytes + cfg.kv_bytes_per_slot() * mean_len + 2 * cfg.hidden
+    step_s = wall / args.steps
     line = {
         'metric': 'batch-1 decode tok/s (Qwen3-1.7B-shape int8); GEMV/attn HBM GB/s vs peak',
         'value': round(value, 2), 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
-        'ms_per_step': round(wall / args.steps * 1e3, 4), 'gpu_ms_per_step': round(gpu_s / args.steps * 1e3, 4),
-        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'int8 weights, bf16 activations, fp32 accumulation',
+        'ms_per_step': round(step_s * 1e3, 4), 'gpu_ms_per_step': round(gpu_s / args.steps * 1e3, 4),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'int8',
         'data': 'synthetic: random-init weights N(0,0.02), uniform-random prompt ids',
-        'config': {'workload': f'{args.model} int8 batch-1 greedy decode, {args.prompt}-token prompt, one graph replay per token',
+        'config': {'workload': f'{args.model} int8 weight-only batch-1 greedy decode, {args.prompt}-token prompt, '
+                               f'one graph replay per token (int8 weights, bf16 activations, fp32 accumulation)',
                    'model': args.model, 'global_batch': 1, 'seq_len': args.prompt + args.warmup + args.steps,
                    'parallelism': 'single GPU'},
         'roofline': roof,
         'cpu_baseline': cpu,
+        'step': {'bytes': int(step_bytes), 'achieved_gbps': round(step_bytes / step_s / 1e9, 1),
+                 'frac': round(step_bytes / step_s / 1e9 / HBM_PEAK_GBPS, 4), 'mean_kv_len': mean_len,
+                 'launches': cfg.layers * (5 if eng.nsplit <= 16 else 6) + 2},
+        'prefill_s': round(prefill_s, 3),
         'streamed_generate': stream,
-        'step_bytes': {'int8_weights': wbytes, 'scales': sbytes, 'kv_per_slot': cfg.kv_bytes_per_slot()},
         'build_s': round(build_s, 1),
+        **extra,
     }
     print(json.dumps(line), flush=True)
 

@@ -50,7 +50,35 @@ SIGNATURES = {
     'egpt_argmax': (_c_int, [_c_vp, _c_int, _c_vp, _c_size, _c_vp, _c_vp, _c_vp]),
     'egpt_qwen3_step_workspace': (_c_int, [_c_vp, ctypes.POINTER(_c_size)]),
     'egpt_qwen3_decode_step': (_c_int, [_c_vp, _c_vp]),
+    'egpt_qwen3_step_gemvs': (_c_int, [_c_vp, _c_vp, _c_int, ctypes.POINTER(_c_int)]),
+    'egpt_int8_gemv_fused_parts': (_c_int, [_c_vp, ctypes.POINTER(_c_int)]),
+    'egpt_int8_gemv_fused': (_c_int, [_c_vp, _c_vp]),
+    'egpt_argmax_parts': (_c_int, [_c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
 }
+
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3
+
+
+class GemvFused(ctypes.Structure):
+    """egpt_gemv_fused: one int8 GEMV of a single row with a fused prologue / epilogue."""
+    _fields_ = [('epilogue', _c_int), ('N', _c_int), ('K', _c_int),
+                ('x', _c_vp), ('x_token', _c_vp), ('x_ld', _c_i64), ('x_rows', _c_int),
+                ('norm_w', _c_vp), ('eps', _c_f),
+                ('merge_m', _c_vp), ('merge_l', _c_vp), ('merge_acc', _c_vp),
+                ('merge_splits', _c_int), ('head_dim', _c_int),
+                ('w', _c_vp), ('ldw', _c_i64), ('scale', _c_vp), ('y', _c_vp),
+                ('resid', _c_vp), ('resid_token', _c_vp), ('resid_ld', _c_i64),
+                ('part_v', _c_vp), ('part_i', _c_vp)]
+
+    def weight_rows(self):
+        """Rows of int8 weights the call streams (SwiGLU reads gate and up rows)."""
+        return 2 * self.N if self.epilogue == EPI_SWIGLU else self.N
+
+    def algorithmic_bytes(self):
+        """Weights + scales + activation in + output out, the int8 GEMV byte model
+        (N K + 4 N + 2 K + 2 N per output row set)."""
+        rows = self.weight_rows()
+        return rows * self.K + 4 * rows + 2 * self.K + 2 * self.N
 
 _LAYER_FIELDS = ('qkv_w', 'qkv_s', 'o_w', 'o_s', 'gu_w', 'gu_s', 'down_w', 'down_s', 'in_norm', 'post_norm',
                  'q_norm', 'k_norm', 'k_cache', 'v_cache')

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kFThreads) void argmax_final_kernel(const float* __
   best = block_argbest<kFWaves>(best);
   if (threadIdx.x == 0) {
     *token = best.i == 0x7fffffff ? 0 : best.i;  // all-NaN logits: token 0
-    *position += 1;
+    if (position) *position += 1;
   }
 }
 
@@ -662,10 +662,185 @@ int launch_attn_step(const AttnStep& a, int G, uint16_t* out, bool merge, hipStr
   return EGPT_LAUNCH_STATUS();
 }
 
+// The public fused-GEMV description -> kernel arguments, validated; then the
+// launch for its (epilogue, norm, source) combination.
+int run_fused(const egpt_gemv_fused& p, hipStream_t st) {
+  if (!p.w || !p.scale || p.N < 1 || p.K < 16 || p.K % 16 || p.K > kMaxChunks * kFChunk || p.ldw < p.K)
+    return EGPT_ERR_INVALID;
+  if (!aligned16(p.w) || p.ldw % 16) return EGPT_ERR_INVALID;
+  const bool merge = p.merge_m != nullptr;
+  const bool norm = p.norm_w != nullptr;
+  if (merge) {
+    if (!p.merge_l || !p.merge_acc || p.merge_splits < 1 || p.merge_splits > kMergeInGemvMaxSplits ||
+        p.head_dim < 8 || p.head_dim % 8 || p.K % p.head_dim || p.K > kGemvWaves * kWave * 8 ||
+        !aligned16(p.merge_acc))
+      return EGPT_ERR_UNSUPPORTED;
+  } else {
+    if (!p.x || !aligned16(p.x) || (p.x_token && (p.x_rows < 1 || p.x_ld % 8))) return EGPT_ERR_INVALID;
+  }
+  if (norm && !aligned16(p.norm_w)) return EGPT_ERR_INVALID;
+  FusedGemv a{};
+  a.x = (const uint16_t*)p.x;
+  a.x_token = p.x_token;
+  a.x_ld = p.x_ld;
+  a.x_rows = p.x_rows > 0 ? p.x_rows : 1;
+  a.norm_w = (const uint16_t*)p.norm_w;
+  a.eps = p.eps;
+  a.w = p.w;
+  a.ldw = p.ldw;
+  a.scale = p.scale;
+  a.N = p.N;
+  a.K = p.K;
+  a.y = (uint16_t*)p.y;
+  a.resid = (const uint16_t*)p.resid;
+  a.resid_token = p.resid_token;
+  a.resid_ld = p.resid_ld;
+  a.part_v = p.part_v;
+  a.part_i = p.part_i;
+  a.ws_m = p.merge_m;
+  a.ws_l = p.merge_l;
+  a.ws_acc = p.merge_acc;
+  a.nsplit = p.merge_splits;
+  a.head_dim = p.head_dim;
+  switch (p.epilogue) {
+    case EGPT_EPI_STORE:
+      if (!p.y || merge) return merge ? EGPT_ERR_UNSUPPORTED : EGPT_ERR_INVALID;
+      return norm ? launch_fused<kEpiStore, true>(a, st) : launch_fused<kEpiStore, false>(a, st);
+    case EGPT_EPI_RESIDUAL:
+      if (!p.y || !p.resid) return EGPT_ERR_INVALID;
+      if (norm) return EGPT_ERR_UNSUPPORTED;
+      return merge ? launch_fused<kEpiResid, false, kXMerge>(a, st) : launch_fused<kEpiResid, false>(a, st);
+    case EGPT_EPI_SWIGLU:
+      if (!p.y) return EGPT_ERR_INVALID;
+      if (!norm || merge) return EGPT_ERR_UNSUPPORTED;
+      return launch_fused<kEpiSwiGLU, true>(a, st);
+    case EGPT_EPI_ARGMAX:
+      if (!p.part_v || !p.part_i) return EGPT_ERR_INVALID;
+      if (!norm || merge) return EGPT_ERR_UNSUPPORTED;
+      return launch_fused<kEpiArgmax, true>(a, st);
+    default:
+      return EGPT_ERR_INVALID;
+  }
+}
+
+// The four fused GEMVs of decode-step layer i, in launch order:
+//   [0] RMSNorm(x; input_layernorm) -> QKV            (layer 0: x = embedding row of *token)
+//   [1] o_proj(merge of the attention partials, or the merged row) + residual -> x
+//   [2] RMSNorm(x; post_attention_layernorm) -> gate/up -> SwiGLU -> act
+//   [3] down_proj(act) + residual -> x
+void layer_gemvs(const egpt_qwen3_step* s, int i, egpt_gemv_fused* g) {
+  const egpt_qwen3_layer& L = s->layer[i];
+  const StepLayout lay = step_layout(s);
+  char* ws = (char*)s->workspace;
+  const bool first = i == 0;
+  const int D = s->head_dim;
+  for (int j = 0; j < 4; ++j) g[j] = egpt_gemv_fused{};
+  g[0].epilogue = EGPT_EPI_STORE;
+  g[0].N = (s->heads + 2 * s->kv_heads) * D;
+  g[0].K = s->hidden;
+  g[0].x = first ? s->embed : s->x;
+  g[0].x_token = first ? s->token : nullptr;
+  g[0].x_ld = s->hidden;
+  g[0].x_rows = s->vocab;
+  g[0].norm_w = L.in_norm;
+  g[0].eps = s->eps;
+  g[0].w = L.qkv_w;
+  g[0].ldw = s->hidden;
+  g[0].scale = L.qkv_s;
+  g[0].y = s->qkv;
+
+  g[1].epilogue = EGPT_EPI_RESIDUAL;
+  g[1].N = s->hidden;
+  g[1].K = s->heads * D;
+  // the o_proj prologue merges the splits itself while each thread owns one
+  // 8-element group of the attention row
+  if (s->nsplit <= kMergeInGemvMaxSplits && s->heads * D <= kGemvWaves * kWave * 8) {
+    g[1].merge_m = (const float*)ws;
+    g[1].merge_l = (const float*)(ws + lay.ml);
+    g[1].merge_acc = (const float*)(ws + 2 * lay.ml);
+    g[1].merge_splits = s->nsplit;
+    g[1].head_dim = D;
+  } else {
+    g[1].x = s->attn;
+  }
+  g[1].w = L.o_w;
+  g[1].ldw = (int64_t)s->heads * D;
+  g[1].scale = L.o_s;
+  g[1].y = s->x;
+  g[1].resid = first ? s->embed : s->x;
+  g[1].resid_token = first ? s->token : nullptr;
+  g[1].resid_ld = s->hidden;
+  g[1].x_rows = s->vocab;
+
+  g[2].epilogue = EGPT_EPI_SWIGLU;
+  g[2].N = s->inter;
+  g[2].K = s->hidden;
+  g[2].x = s->x;
+  g[2].norm_w = L.post_norm;
+  g[2].eps = s->eps;
+  g[2].w = L.gu_w;
+  g[2].ldw = s->hidden;
+  g[2].scale = L.gu_s;
+  g[2].y = s->act;
+
+  g[3].epilogue = EGPT_EPI_RESIDUAL;
+  g[3].N = s->hidden;
+  g[3].K = s->inter;
+  g[3].x = s->act;
+  g[3].w = L.down_w;
+  g[3].ldw = s->inter;
+  g[3].scale = L.down_s;
+  g[3].y = s->x;
+  g[3].resid = s->x;
+}
+
+// The head GEMV: RMSNorm(x; norm) -> lm_head -> logits and per-block maxima.
+void head_gemv(const egpt_qwen3_step* s, egpt_gemv_fused* g) {
+  const StepLayout lay = step_layout(s);
+  char* ws = (char*)s->workspace;
+  *g = egpt_gemv_fused{};
+  g->epilogue = EGPT_EPI_ARGMAX;
+  g->N = s->vocab;
+  g->K = s->hidden;
+  g->x = s->x;
+  g->norm_w = s->final_norm;
+  g->eps = s->eps;
+  g->w = s->head_w;
+  g->ldw = s->hidden;
+  g->scale = s->head_s;
+  g->y = s->logits;
+  g->part_v = (float*)(ws + 2 * lay.ml + lay.acc);
+  g->part_i = (int*)(ws + 2 * lay.ml + lay.acc + lay.part_v);
+}
+
+void step_gemvs(const egpt_qwen3_step* s, egpt_gemv_fused* out) {
+  for (int i = 0; i < s->layers; ++i) layer_gemvs(s, i, out + 4 * i);
+  head_gemv(s, out + 4 * s->layers);
+}
+
 }  // namespace
 }  // namespace egpt
 
 using namespace egpt;
+
+extern "C" int egpt_int8_gemv_fused_parts(const egpt_gemv_fused* g, int* parts) {
+  if (!g || !parts || g->N < 1) return EGPT_ERR_INVALID;
+  *parts = g->epilogue == EGPT_EPI_ARGMAX ? (int)gemv_blocks(g->N, false, true) : 0;
+  return EGPT_OK;
+}
+
+extern "C" int egpt_int8_gemv_fused(const egpt_gemv_fused* g, hipStream_t stream) {
+  if (!g) return EGPT_ERR_INVALID;
+  return run_fused(*g, stream);
+}
+
+extern "C" int egpt_argmax_parts(const float* part_v, const int* part_i, int parts, int64_t* token,
+                                 int64_t* position, hipStream_t stream) {
+  if (!part_v || !part_i || !token || parts < 1) return EGPT_ERR_INVALID;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kFThreads), 0, stream, part_v, part_i, parts, token,
+                     position);
+  return EGPT_LAUNCH_STATUS();
+}
 
 extern "C" int egpt_qwen3_step_workspace(const egpt_qwen3_step* s, size_t* bytes) {
   if (!s || !bytes || s->heads < 1 || s->kv_heads < 1 || s->nsplit < 1 || s->head_dim < 1 || s->vocab < 1)
@@ -674,40 +849,31 @@ extern "C" int egpt_qwen3_step_workspace(const egpt_qwen3_step* s, size_t* bytes
   return EGPT_OK;
 }
 
+extern "C" int egpt_qwen3_step_gemvs(const egpt_qwen3_step* s, egpt_gemv_fused* out, int capacity, int* count) {
+  if (!count) return EGPT_ERR_INVALID;
+  const int st = check_step(s);
+  if (st != EGPT_OK) return st;
+  *count = 4 * s->layers + 1;
+  if (!out) return EGPT_OK;
+  if (capacity < *count) return EGPT_ERR_INVALID;
+  step_gemvs(s, out);
+  return EGPT_OK;
+}
+
 extern "C" int egpt_qwen3_decode_step(const egpt_qwen3_step* s, hipStream_t stream) {
   int st = check_step(s);
   if (st != EGPT_OK) return st;
   const StepLayout lay = step_layout(s);
   char* ws = (char*)s->workspace;
-  float* ws_m = (float*)ws;
-  float* ws_l = (float*)(ws + lay.ml);
-  float* ws_acc = (float*)(ws + 2 * lay.ml);
-  float* part_v = (float*)(ws + 2 * lay.ml + lay.acc);
-  int* part_i = (int*)(ws + 2 * lay.ml + lay.acc + lay.part_v);
-
   const int D = s->head_dim;
   const int G = s->heads / s->kv_heads;
-  const int n_qkv = (s->heads + 2 * s->kv_heads) * D;
-  const uint16_t* x = (const uint16_t*)s->x;
+  egpt_gemv_fused g[4];
   for (int i = 0; i < s->layers; ++i) {
     const egpt_qwen3_layer& L = s->layer[i];
-    const bool first = i == 0;
+    layer_gemvs(s, i, g);
     // 1. RMSNorm + QKV
-    FusedGemv g{};
-    g.x = first ? (const uint16_t*)s->embed : x;
-    g.x_token = first ? s->token : nullptr;
-    g.x_ld = s->hidden;
-    g.x_rows = s->vocab;
-    g.norm_w = (const uint16_t*)L.in_norm;
-    g.eps = s->eps;
-    g.w = L.qkv_w;
-    g.ldw = s->hidden;
-    g.scale = L.qkv_s;
-    g.N = n_qkv;
-    g.K = s->hidden;
-    g.y = (uint16_t*)s->qkv;
-    if ((st = launch_fused<kEpiStore, true>(g, stream)) != EGPT_OK) return st;
-    // 2. attention
+    if ((st = run_fused(g[0], stream)) != EGPT_OK) return st;
+    // 2. attention partials (and their merge, when the o_proj prologue does not merge)
     AttnStep at{};
     at.qkv = (const uint16_t*)s->qkv;
     at.q_norm_w = (const uint16_t*)L.q_norm;
@@ -719,85 +885,28 @@ extern "C" int egpt_qwen3_decode_step(const egpt_qwen3_step* s, hipStream_t stre
     at.v_cache = (uint16_t*)L.v_cache;
     at.c_sh = (int64_t)s->cap * D;
     at.c_sn = D;
-    at.ws_m = ws_m;
-    at.ws_l = ws_l;
-    at.ws_acc = ws_acc;
+    at.ws_m = (float*)ws;
+    at.ws_l = (float*)(ws + lay.ml);
+    at.ws_acc = (float*)(ws + 2 * lay.ml);
     at.Hkv = s->kv_heads;
     at.cap = s->cap;
     at.nsplit = s->nsplit;
     at.eps = s->eps;
     at.scale = 1.0f / sqrtf((float)D);
     uint16_t* attn_out = (uint16_t*)s->attn;
-    // the o_proj prologue merges the splits itself while each thread owns one
-    // 8-element group of the attention row (heads * head_dim <= 8 per thread)
-    const bool merge_in_gemv =
-        s->nsplit <= kMergeInGemvMaxSplits && s->heads * D <= kGemvWaves * kWave * 8;
+    const bool merge_in_gemv = g[1].merge_m != nullptr;
     if (D == 128) st = launch_attn_step<128>(at, G, attn_out, !merge_in_gemv, stream);
     else if (D == 64) st = launch_attn_step<64>(at, G, attn_out, !merge_in_gemv, stream);
     else st = launch_attn_step<32>(at, G, attn_out, !merge_in_gemv, stream);
     if (st != EGPT_OK) return st;
-    // 3. o_proj + residual (layer 0: the residual is the embedding row)
-    FusedGemv o{};
-    o.x = (const uint16_t*)s->attn;
-    o.x_rows = s->vocab;
-    o.w = L.o_w;
-    o.ldw = (int64_t)s->heads * D;
-    o.scale = L.o_s;
-    o.N = s->hidden;
-    o.K = s->heads * D;
-    o.y = (uint16_t*)s->x;
-    o.resid = first ? (const uint16_t*)s->embed : x;
-    o.resid_token = first ? s->token : nullptr;
-    o.resid_ld = s->hidden;
-    o.ws_m = ws_m;
-    o.ws_l = ws_l;
-    o.ws_acc = ws_acc;
-    o.nsplit = s->nsplit;
-    o.head_dim = D;
-    st = merge_in_gemv ? launch_fused<kEpiResid, false, kXMerge>(o, stream) : launch_fused<kEpiResid, false>(o, stream);
-    if (st != EGPT_OK) return st;
-    // 4. RMSNorm + gate/up + SwiGLU
-    FusedGemv gu{};
-    gu.x = x;
-    gu.x_rows = 1;
-    gu.norm_w = (const uint16_t*)L.post_norm;
-    gu.eps = s->eps;
-    gu.w = L.gu_w;
-    gu.ldw = s->hidden;
-    gu.scale = L.gu_s;
-    gu.N = s->inter;
-    gu.K = s->hidden;
-    gu.y = (uint16_t*)s->act;
-    if ((st = launch_fused<kEpiSwiGLU, true>(gu, stream)) != EGPT_OK) return st;
-    // 5. down + residual
-    FusedGemv dn{};
-    dn.x = (const uint16_t*)s->act;
-    dn.x_rows = 1;
-    dn.w = L.down_w;
-    dn.ldw = s->inter;
-    dn.scale = L.down_s;
-    dn.N = s->hidden;
-    dn.K = s->inter;
-    dn.y = (uint16_t*)s->x;
-    dn.resid = x;
-    if ((st = launch_fused<kEpiResid, false>(dn, stream)) != EGPT_OK) return st;
+    // 3. o_proj + residual, 4. RMSNorm + gate/up + SwiGLU, 5. down + residual
+    for (int j = 1; j < 4; ++j)
+      if ((st = run_fused(g[j], stream)) != EGPT_OK) return st;
   }
   // head: final norm + lm_head + per-block maxima, then the greedy pick
-  FusedGemv h{};
-  h.x = x;
-  h.x_rows = 1;
-  h.norm_w = (const uint16_t*)s->final_norm;
-  h.eps = s->eps;
-  h.w = s->head_w;
-  h.ldw = s->hidden;
-  h.scale = s->head_s;
-  h.N = s->vocab;
-  h.K = s->hidden;
-  h.y = (uint16_t*)s->logits;
-  h.part_v = part_v;
-  h.part_i = part_i;
-  if ((st = launch_fused<kEpiArgmax, true>(h, stream)) != EGPT_OK) return st;
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kFThreads), 0, stream, part_v, part_i,
+  head_gemv(s, g);
+  if ((st = run_fused(g[0], stream)) != EGPT_OK) return st;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kFThreads), 0, stream, g[0].part_v, g[0].part_i,
                      (int)head_blocks(s->vocab), s->token, s->position);
   return EGPT_LAUNCH_STATUS();
 }

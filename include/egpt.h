@@ -138,6 +138,66 @@ int egpt_argmax(const void *logits, int n, void *workspace, size_t workspace_byt
                 int64_t *position, hipStream_t stream);
 
 /*
+ * One int8 weight-only GEMV of a single activation row (M = 1) with a fused
+ * prologue and epilogue: the building block of the decode step below, and the
+ * batch-1 form of the reference's int8 linear (research/realmodel/int8_linear.py:26-38,
+ * y = bf16(s * fp32 sum)) with the elementwise work around it
+ * (transformers' Qwen3 RMSNorm / residual / SwiGLU, models/qwen3/modeling_qwen3.py).
+ *
+ * Activation (bf16, K elements), one of:
+ *   x                       the row x[0..K)
+ *   x + *x_token * x_ld     a table row selected on the device (token clamped to [0, x_rows))
+ *   merge_m/_l/_acc != NULL the split-K attention partials of K / head_dim heads
+ *                           (merge_splits splits, the layout of egpt_decode_attn's
+ *                           workspace for B = 1), merged as in the combine
+ * optionally RMS-normalised first: h = bf16(norm_w * bf16(x * rsqrt(mean x^2 + eps))).
+ * Epilogue on the fp32 sums acc[n] (weights int8 [rows, K] with row stride ldw,
+ * fp32 scale per row):
+ *   EGPT_EPI_STORE     y[n] = bf16(scale[n] acc[n])                         n < N
+ *   EGPT_EPI_RESIDUAL  y[n] = bf16(resid[n] + bf16(scale[n] acc[n]))       (resid: row, or table row
+ *                      by *resid_token like x; y may alias resid)
+ *   EGPT_EPI_SWIGLU    y[n] = bf16(bf16(silu(g)) * u), g = bf16(scale[n] acc[n]) from row n,
+ *                      u = bf16(scale[N + n] acc[N + n]) from row N + n    (rows 2N)
+ *   EGPT_EPI_ARGMAX    y[n] = bf16(scale[n] acc[n]) if y != NULL, and per-block maxima
+ *                      (value, first index) to part_v / part_i (egpt_int8_gemv_fused_parts
+ *                      entries); egpt_argmax_parts() then picks the token.
+ * Supported: STORE with or without norm; RESIDUAL from a row or a merge, no
+ * norm; SWIGLU and ARGMAX with norm. K a multiple of 16, K <= 12288 (merge:
+ * K <= 4096, merge_splits <= 16); 16-byte aligned x, norm_w, w rows, merge_acc.
+ */
+enum { EGPT_EPI_STORE = 0, EGPT_EPI_RESIDUAL = 1, EGPT_EPI_SWIGLU = 2, EGPT_EPI_ARGMAX = 3 };
+
+typedef struct egpt_gemv_fused {
+  int epilogue;
+  int N, K;
+  const void *x;
+  const int64_t *x_token;
+  int64_t x_ld;
+  int x_rows;
+  const void *norm_w;
+  float eps;
+  const float *merge_m, *merge_l, *merge_acc;
+  int merge_splits, head_dim;
+  const int8_t *w;
+  int64_t ldw;
+  const float *scale;
+  void *y;
+  const void *resid;
+  const int64_t *resid_token;
+  int64_t resid_ld;
+  float *part_v;
+  int *part_i;
+} egpt_gemv_fused;
+
+int egpt_int8_gemv_fused_parts(const egpt_gemv_fused *g, int *parts);
+int egpt_int8_gemv_fused(const egpt_gemv_fused *g, hipStream_t stream);
+
+/* Greedy pick over per-block maxima: *token = index of the largest value
+ * (first index on ties, torch.argmax), *position += 1 when position != NULL. */
+int egpt_argmax_parts(const float *part_v, const int *part_i, int parts, int64_t *token, int64_t *position,
+                      hipStream_t stream);
+
+/*
  * Whole batch-1 decode step of a Qwen3 decoder with int8 weight-only linears,
  * fused into 5 launches per layer plus one for the head (RMSNorm in the GEMV
  * prologues; residual adds and SwiGLU in the GEMV epilogues; q/k-norm, RoPE,
@@ -203,6 +263,12 @@ typedef struct egpt_qwen3_step {
 
 int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
 int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
+
+/* The step's fused GEMV launches as egpt_gemv_fused descriptions, in launch
+ * order (4 per layer, then the head): *count = 4 layers + 1; `out` (capacity
+ * entries) may be NULL to query the count. Replaying them through
+ * egpt_int8_gemv_fused runs exactly the GEMVs of egpt_qwen3_decode_step. */
+int egpt_qwen3_step_gemvs(const egpt_qwen3_step *step, egpt_gemv_fused *out, int capacity, int *count);
 
 #ifdef __cplusplus
 }
