@@ -23,47 +23,101 @@
 namespace egpt {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnUnroll = 4;  // slots per group per iteration; double-buffered, so 2 x 4 K and V rows in flight
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <typename T, int D>
+// Geometry of one attention block of NT threads over rows of D elements of T:
+// a lane issues LPR 16-byte loads per K (and V) row, so it owns EPL contiguous
+// elements; LPS lanes cover a row; the block runs NG independent softmax
+// streams, each advancing U slots per iteration.
+//   LPR 1: 16 lanes per 128-element bf16 row, every load instruction of a
+//          wavefront reads 1 KiB of 4 consecutive rows (the layout used).
+//   LPR > 1: fewer lanes per row, each owning LPR * 16 contiguous bytes: less
+//          cross-lane reduction and softmax work per slot, but every load
+//          instruction then touches 16 rows; measured slower on the MI355X
+//          with non-temporal loads (41 vs 24 us at L = 32768), so kept only as
+//          a tuning option.
+// For bf16, q . k runs on packed bf16 pairs (v_dot2_f32_bf16) in either layout.
+template <typename T, int D, int NT = kAttnThreads, int LPR = 1, int U = 4>
 struct AttnGeom {
-  static constexpr int EPL = 16 / Elem<T>::kBytes;  // elements per 16-byte lane load
+  static constexpr int EPV = 16 / Elem<T>::kBytes;  // elements per 16-byte load
+  static constexpr int EPL = EPV * LPR;             // elements per lane
   static constexpr int LPS = D / EPL;               // lanes per slot
-  static constexpr int NG = kAttnThreads / LPS;     // independent softmax streams per block
-  static_assert(LPS >= 1 && LPS <= 64 && (kWave % LPS) == 0, "unsupported head dim / dtype");
+  static constexpr int NG = NT / LPS;               // independent softmax streams per block
+  static constexpr int kUnroll = U;
+  static_assert(LPS >= 1 && LPS <= 64 && (kWave % LPS) == 0 && D % EPL == 0, "unsupported head dim / layout");
 };
+
+template <typename T>
+constexpr bool kAttnDot2 = __is_same(T, __bf16);  // q . k on packed bf16 pairs
 
 // K/V rows in flight for one softmax stream (register double buffer).
+template <int LPR, int U>
 struct AttnPipe {
-  u32x4 kr[kAttnUnroll], vr[kAttnUnroll];
+  u32x4 kr[U][LPR], vr[U][LPR];
 };
 
-template <typename T, int D>
-__device__ __forceinline__ void attn_issue(AttnPipe& pp, const T* __restrict__ kb, int64_t k_sn,
+template <typename Geo, typename T, int LPR, int U>
+__device__ __forceinline__ void attn_issue(AttnPipe<LPR, U>& pp, const T* __restrict__ kb, int64_t k_sn,
                                            const T* __restrict__ vb, int64_t v_sn, int64_t base, int64_t end) {
-  constexpr int NG = AttnGeom<T, D>::NG;
 #pragma unroll
-  for (int u = 0; u < kAttnUnroll; ++u) {
-    const int64_t n = base + (int64_t)u * NG;
+  for (int u = 0; u < U; ++u) {
+    const int64_t n = base + (int64_t)u * Geo::NG;
     const int64_t nn = n < end ? n : base;  // never touch slots past the live range
-    pp.kr[u] = ld16(kb + nn * k_sn);
-    pp.vr[u] = ld16(vb + nn * v_sn);
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) {
+      // K and V are read once per call: non-temporal loads stream them past
+      // the caches (measured 5.5 vs 4.9 TB/s at L = 32768, 16 q / 8 kv heads)
+      pp.kr[u][j] = ld16_stream(kb + nn * k_sn + j * Geo::EPV);
+      pp.vr[u][j] = ld16_stream(vb + nn * v_sn + j * Geo::EPV);
+    }
   }
 }
 
 // Issue this thread's first K/V loads of slots [start, end); attn_partial()
 // continues from them. Splitting the two lets a caller overlap the first round
 // trip with work of its own (computing the query).
-template <typename T, int D>
-__device__ __forceinline__ void attn_begin(AttnPipe& pp, const T* __restrict__ kbase, int64_t k_sn,
+template <typename Geo, typename T, int LPR, int U>
+__device__ __forceinline__ void attn_begin(AttnPipe<LPR, U>& pp, const T* __restrict__ kbase, int64_t k_sn,
                                            const T* __restrict__ vbase, int64_t v_sn, int64_t start, int64_t end) {
-  constexpr int EPL = AttnGeom<T, D>::EPL;
-  constexpr int LPS = AttnGeom<T, D>::LPS;
   const int tid = threadIdx.x;
-  const int d0 = (tid % LPS) * EPL;
-  const int64_t n0 = start + tid / LPS;
-  if (n0 < end) attn_issue<T, D>(pp, kbase + d0, k_sn, vbase + d0, v_sn, n0, end);
+  const int d0 = (tid % Geo::LPS) * Geo::EPL;
+  const int64_t n0 = start + tid / Geo::LPS;
+  if (n0 < end) attn_issue<Geo>(pp, kbase + d0, k_sn, vbase + d0, v_sn, n0, end);
+}
+
+// Packed bf16 pairs of EPL fp32 values that are exact bf16 (queries, new keys).
+template <int EPL>
+__device__ __forceinline__ void pack_bf16(const float (&x)[EPL], uint32_t (&p)[EPL / 2]) {
+#pragma unroll
+  for (int i = 0; i < EPL / 2; ++i) p[i] = (uint32_t)f32_to_bf16(x[2 * i]) | ((uint32_t)f32_to_bf16(x[2 * i + 1]) << 16);
+}
+
+// This lane's share of q . k for one slot: fp32 products and sums (bf16 pairs
+// through v_dot2_f32_bf16 when T is bf16).
+template <typename Geo, typename T, int LPR>
+__device__ __forceinline__ float attn_qk(const u32x4 (&kr)[LPR], const float (&qf)[Geo::EPL],
+                                         const uint32_t (&qp)[Geo::EPL / 2]) {
+  float p = 0.f;
+  if constexpr (kAttnDot2<T>) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) {
+      const uint32_t w[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w[i]),
+                                            __builtin_bit_cast(bf16x2_t, qp[4 * j + i]), p, false);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) {
+      float kf[Geo::EPV];
+      Elem<T>::unpack(kr[j], kf);
+#pragma unroll
+      for (int e = 0; e < Geo::EPV; ++e) p = fmaf(qf[j * Geo::EPV + e], kf[e], p);
+    }
+  }
+  return p;
 }
 
 // One block's partial softmax state over slots [start, end) of one kv head, for
@@ -76,22 +130,29 @@ __device__ __forceinline__ void attn_begin(AttnPipe& pp, const T* __restrict__ k
 //   ws_m[row + g * nsplit], ws_l[...], ws_acc[(row + g * nsplit) * D + d]
 // where row = (b * Hq + hk * G) * nsplit + split. An empty range with no extra
 // slot gives the empty state (m = -inf, l = 0, acc = 0). Must be called by all
-// 256 threads.
-template <typename T, int D, int G>
-__device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>::EPL], AttnPipe& pp,
+// NT threads of the block.
+template <typename Geo, typename T, int G, int LPR, int U>
+__device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], AttnPipe<LPR, U>& pp,
                                              const T* __restrict__ kbase, int64_t k_sn, const T* __restrict__ vbase,
                                              int64_t v_sn, int64_t start, int64_t end, float scale,
                                              float* __restrict__ ws_m, float* __restrict__ ws_l,
                                              float* __restrict__ ws_acc, int64_t row, int nsplit,
                                              const float* xk = nullptr, const float* xv = nullptr) {
-  constexpr int EPL = AttnGeom<T, D>::EPL;
-  constexpr int LPS = AttnGeom<T, D>::LPS;
-  constexpr int NG = AttnGeom<T, D>::NG;
+  constexpr int EPL = Geo::EPL;
+  constexpr int EPV = Geo::EPV;
+  constexpr int LPS = Geo::LPS;
+  constexpr int NG = Geo::NG;
+  constexpr int NT = NG * LPS;
+  constexpr int D = EPL * LPS;
   const int tid = threadIdx.x;
   const int grp = tid / LPS;
   const int d0 = (tid % LPS) * EPL;
   kbase += d0;
   vbase += d0;
+
+  uint32_t qp[G][EPL / 2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) pack_bf16<EPL>(qf[g], qp[g]);
 
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -102,48 +163,46 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
   }
 
-  constexpr int64_t kStep = (int64_t)NG * kAttnUnroll;  // slots one group advances per iteration
+  constexpr int64_t kStep = (int64_t)NG * U;  // slots one stream advances per iteration
   // Register double buffer: the loads of iteration i+1 are issued before the
-  // arithmetic of iteration i, so each wavefront keeps 2 * kAttnUnroll K and V
-  // rows in flight instead of waiting on every round trip.
+  // arithmetic of iteration i.
   for (int64_t n0 = start + grp; n0 < end; n0 += kStep) {
-    u32x4 kc[kAttnUnroll], vc[kAttnUnroll];
+    u32x4 kc[U][LPR], vc[U][LPR];
 #pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) {
-      kc[u] = pp.kr[u];
-      vc[u] = pp.vr[u];
-    }
-    if (n0 + kStep < end) attn_issue<T, D>(pp, kbase, k_sn, vbase, v_sn, n0 + kStep, end);
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < LPR; ++j) {
+        kc[u][j] = pp.kr[u][j];
+        vc[u][j] = pp.vr[u][j];
+      }
+    if (n0 + kStep < end) attn_issue<Geo>(pp, kbase, k_sn, vbase, v_sn, n0 + kStep, end);
 
-    float s[kAttnUnroll][G];
+    float s[U][G];
 #pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const bool valid = n0 + (int64_t)u * NG < end;
-      float kf[EPL];
-      Elem<T>::unpack(kc[u], kf);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float p = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], kf[e], p);
-        p = group_sum<LPS>(p) * scale;  // the reference's fp32 logit: (q . k) * scale
-        s[u][g] = valid ? p : -INFINITY;
+        const float p = group_sum<LPS>(attn_qk<Geo, T, LPR>(kc[u], qf[g], qp[g])) * scale;
+        s[u][g] = valid ? p : -INFINITY;  // the reference's fp32 logit: (q . k) * scale
       }
     }
-    float vf[kAttnUnroll][EPL];
+    float vf[U][EPL];
 #pragma unroll
-    for (int u = 0; u < kAttnUnroll; ++u) Elem<T>::unpack(vc[u], vf[u]);
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < LPR; ++j) Elem<T>::unpack(vc[u][j], &vf[u][j * EPV]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mt = m[g];
 #pragma unroll
-      for (int u = 0; u < kAttnUnroll; ++u) mt = fmaxf(mt, s[u][g]);
+      for (int u = 0; u < U; ++u) mt = fmaxf(mt, s[u][g]);
       // slot n0 is always valid, so mt is finite
       const float alpha = exp2f((m[g] - mt) * kLog2e);
-      float p[kAttnUnroll];
+      float p[U];
       float psum = 0.f;
 #pragma unroll
-      for (int u = 0; u < kAttnUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         p[u] = exp2f((s[u][g] - mt) * kLog2e);  // 0 for invalid slots
         psum += p[u];
       }
@@ -152,7 +211,7 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
       for (int e = 0; e < EPL; ++e) {
         float a = acc[g][e] * alpha;
 #pragma unroll
-        for (int u = 0; u < kAttnUnroll; ++u) a = fmaf(p[u], vf[u][e], a);
+        for (int u = 0; u < U; ++u) a = fmaf(p[u], vf[u][e], a);
         acc[g][e] = a;
       }
       m[g] = mt;
@@ -160,11 +219,24 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
   }
 
   if (xk) {  // block-uniform: the extra slot goes to stream 0
+    uint32_t xkp[EPL / 2];
+    float xkf[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) xkf[e] = xk[e];
+    pack_bf16<EPL>(xkf, xkp);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float p = 0.f;
+      if constexpr (kAttnDot2<T>) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], xk[e], p);
+        for (int i = 0; i < EPL / 2; ++i)
+          p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, xkp[i]),
+                                              __builtin_bit_cast(bf16x2_t, qp[g][i]), p, false);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], xk[e], p);
+      }
       const float sx = group_sum<LPS>(p) * scale;
       if (grp == 0) {
         const float mt = fmaxf(m[g], sx);
@@ -199,8 +271,8 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
     }
   }
 
-  // Merge the 4 wavefronts through LDS and write this split's partial state.
-  constexpr int kWaves = kAttnThreads / kWave;
+  // Merge the wavefronts through LDS and write this split's partial state.
+  constexpr int kWaves = NT / kWave;
   __shared__ float sm_m[kWaves][G];
   __shared__ float sm_l[kWaves][G];
   __shared__ float sm_acc[kWaves][G][D];
@@ -218,7 +290,7 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
     }
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += kAttnThreads) {
+  for (int i = tid; i < G * D; i += NT) {
     const int g = i / D;
     const int d = i % D;
     float mx = -INFINITY;
@@ -242,22 +314,70 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][AttnGeom<T, D>
   }
 }
 
-// The partial-softmax reduce of one (row, query head) at element d:
-// out = sum_s w_s acc_s[d] / sum_s w_s l_s with w_s = exp(m_s - max m).
-// Splits are visited in order, so the result does not depend on timing.
-__device__ __forceinline__ float attn_combine_one(const float* __restrict__ mrow, const float* __restrict__ lrow,
-                                                  const float* __restrict__ arow, int nsplit, int D, int d) {
+// The partial-softmax reduce of one (row, query head),
+//   out[d] = sum_s w_s acc_s[d] / sum_s w_s l_s,  w_s = exp(m_s - max_j m_j),
+// for all D elements by a block of NT threads. The splits are dealt round-robin to NT / D thread groups (one thread
+// per element d in each group); a group walks its splits 8 at a time with
+// independent loads, and the groups' sums are added in group order, so the
+// result is fixed for a given split count. Returns true on the threads of group
+// 0, whose `out` holds element d = threadIdx.x. Empty splits carry m = -inf,
+// l = 0 and acc = 0, so their weight and terms are 0. Call from all NT threads.
+template <int D, int NT>
+__device__ __forceinline__ bool attn_combine_block(const float* __restrict__ mrow, const float* __restrict__ lrow,
+                                                   const float* __restrict__ arow, int nsplit, float& out) {
+  static_assert(NT % D == 0 && NT % kWave == 0, "block must tile the head dimension");
+  constexpr int kParts = NT / D;
+  constexpr int kUn = 8;
+  __shared__ float red[NT / kWave];
+  __shared__ float part_a[kParts][D];
+  __shared__ float part_l[kParts];
+  const int tid = threadIdx.x;
+  const int d = tid % D;
+  const int part = tid / D;
   float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, mrow[s]);
+  for (int s = tid; s < nsplit; s += NT) mx = fmaxf(mx, mrow[s]);
+  mx = wave_max(mx);
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int j = 1; j < NT / kWave; ++j) mx = fmaxf(mx, red[j]);
   float a = 0.f, ls = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float ms = mrow[s];
-    if (ms == -INFINITY) continue;  // empty split: weight 0
-    const float wgt = exp2f((ms - mx) * kLog2e);
+  int s = part;
+  for (; s + (kUn - 1) * kParts < nsplit; s += kUn * kParts) {
+    float ms[kUn], lv[kUn], av[kUn];
+#pragma unroll
+    for (int u = 0; u < kUn; ++u) {
+      const int su = s + u * kParts;
+      ms[u] = mrow[su];
+      lv[u] = lrow[su];
+      av[u] = arow[(int64_t)su * D + d];
+    }
+#pragma unroll
+    for (int u = 0; u < kUn; ++u) {
+      const float wgt = ms[u] == -INFINITY ? 0.f : exp2f((ms[u] - mx) * kLog2e);
+      a = fmaf(wgt, av[u], a);
+      ls = fmaf(wgt, lv[u], ls);
+    }
+  }
+  for (; s < nsplit; s += kParts) {
+    const float msv = mrow[s];
+    const float wgt = msv == -INFINITY ? 0.f : exp2f((msv - mx) * kLog2e);
     a = fmaf(wgt, arow[(int64_t)s * D + d], a);
     ls = fmaf(wgt, lrow[s], ls);
   }
-  return a / ls;
+  part_a[part][d] = a;
+  if (d == 0) part_l[part] = ls;
+  __syncthreads();
+  if (part != 0) return false;
+  float at = part_a[0][d], lt = part_l[0];
+#pragma unroll
+  for (int p = 1; p < kParts; ++p) {
+    at += part_a[p][d];
+    lt += part_l[p];
+  }
+  out = at / lt;
+  return true;
 }
 
 // Split `len` live slots into `nsplit` contiguous pieces; piece `split` is [start, end).

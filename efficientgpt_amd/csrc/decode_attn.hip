@@ -13,15 +13,25 @@
 namespace egpt {
 namespace {
 
-template <typename T, int D, int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
+// One 16-byte load per lane per K/V row, 4 slots per stream per iteration: the
+// fastest layout of a cold sweep (L 4096 / 32768, 16 q / 8 kv heads, D 128).
+template <typename T>
+constexpr int kSplitLPR = 1;
+template <typename T>
+constexpr int kSplitUnroll = 4;
+
+template <typename T, int D, int G, int NT = kAttnThreads>
+__global__ __launch_bounds__(NT) void attn_split_kernel(
     const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ k, int64_t k_sb, int64_t k_sh,
     int64_t k_sn, const T* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
     const int64_t* __restrict__ position, int64_t pos_stride, float* __restrict__ ws_m, float* __restrict__ ws_l,
     float* __restrict__ ws_acc, int Hkv, int cap, int nsplit, float scale) {
-  constexpr int EPL = AttnGeom<T, D>::EPL;
-  constexpr int LPS = AttnGeom<T, D>::LPS;
-  const int d0 = (threadIdx.x % LPS) * EPL;
+  constexpr int LPR = kSplitLPR<T>;
+  constexpr int U = kSplitUnroll<T>;
+  using Geo = AttnGeom<T, D, NT, LPR, U>;
+  constexpr int EPL = Geo::EPL;
+  constexpr int EPV = Geo::EPV;
+  const int d0 = (threadIdx.x % Geo::LPS) * EPL;
   const int bh = blockIdx.x;  // b * Hkv + kv head
   const int b = bh / Hkv;
   const int hk = bh % Hkv;
@@ -33,33 +43,40 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(
   int64_t start, end;
   attn_split_range(len, nsplit, split, start, end);
 
-  u32x4 qr[G];
+  u32x4 qr[G][LPR];
 #pragma unroll
-  for (int g = 0; g < G; ++g) qr[g] = ld16(q + (int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d0);
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) qr[g][j] = ld16(q + (int64_t)b * q_sb + (int64_t)(hk * G + g) * q_sh + d0 + j * EPV);
   const T* kb = k + (int64_t)b * k_sb + (int64_t)hk * k_sh;
   const T* vb = v + (int64_t)b * v_sb + (int64_t)hk * v_sh;
-  AttnPipe pp;
-  attn_begin<T, D>(pp, kb, k_sn, vb, v_sn, start, end);
+  AttnPipe<LPR, U> pp;
+  attn_begin<Geo>(pp, kb, k_sn, vb, v_sn, start, end);
   float qf[G][EPL];
 #pragma unroll
-  for (int g = 0; g < G; ++g) Elem<T>::unpack(qr[g], qf[g]);
-  attn_partial<T, D, G>(qf, pp, kb, k_sn, vb, v_sn, start, end, scale, ws_m, ws_l, ws_acc,
-                        ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit);
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) Elem<T>::unpack(qr[g][j], &qf[g][j * EPV]);
+  attn_partial<Geo, T, G>(qf, pp, kb, k_sn, vb, v_sn, start, end, scale, ws_m, ws_l, ws_acc,
+                          ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit);
 }
 
-// Partial-softmax reduce: one block per (b, query head), one thread per d.
+// Partial-softmax reduce: one block of kCombineThreads per (b, query head).
+constexpr int kCombineThreads = 256;
+
 template <typename T, int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ ws_m,
-                                                         const float* __restrict__ ws_l,
-                                                         const float* __restrict__ ws_acc, T* __restrict__ out,
-                                                         int64_t o_sb, int64_t o_sh, int Hq, int nsplit) {
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const float* __restrict__ ws_m,
+                                                                       const float* __restrict__ ws_l,
+                                                                       const float* __restrict__ ws_acc,
+                                                                       T* __restrict__ out, int64_t o_sb, int64_t o_sh,
+                                                                       int Hq, int nsplit) {
   const int bh = blockIdx.x;
   const int b = bh / Hq;
   const int h = bh % Hq;
-  const int d = threadIdx.x;
-  const float r = attn_combine_one(ws_m + (int64_t)bh * nsplit, ws_l + (int64_t)bh * nsplit,
-                                   ws_acc + (int64_t)bh * nsplit * D, nsplit, D, d);
-  Elem<T>::store1(out + (int64_t)b * o_sb + (int64_t)h * o_sh + d, r);
+  float r;
+  if (attn_combine_block<D, kCombineThreads>(ws_m + (int64_t)bh * nsplit, ws_l + (int64_t)bh * nsplit,
+                                             ws_acc + (int64_t)bh * nsplit * D, nsplit, r))
+    Elem<T>::store1(out + (int64_t)b * o_sb + (int64_t)h * o_sh + threadIdx.x, r);
 }
 
 struct AttnArgs {
@@ -81,8 +98,8 @@ int launch_attn(const AttnArgs& a, hipStream_t st) {
                      (const T*)a.k, a.k_sb, a.k_sh, a.k_sn, (const T*)a.v, a.v_sb, a.v_sh, a.v_sn, a.position,
                      a.pos_stride, a.ws_m, a.ws_l, a.ws_acc, a.Hkv, a.cap, a.nsplit, a.scale);
   if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
-  hipLaunchKernelGGL((attn_combine_kernel<T, D>), dim3((unsigned)(a.B * a.Hq)), dim3(D), 0, st, a.ws_m, a.ws_l,
-                     a.ws_acc, (T*)a.out, a.o_sb, a.o_sh, a.Hq, a.nsplit);
+  hipLaunchKernelGGL((attn_combine_kernel<T, D>), dim3((unsigned)(a.B * a.Hq)), dim3(kCombineThreads), 0, st,
+                     a.ws_m, a.ws_l, a.ws_acc, (T*)a.out, a.o_sb, a.o_sh, a.Hq, a.nsplit);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -119,11 +136,12 @@ using namespace egpt;
 
 extern "C" int egpt_decode_attn_default_splits(int B, int Hkv, int cap) {
   if (B < 1 || Hkv < 1 || cap < 1) return 1;
-  // At least one block-iteration (4 wavefronts x 16 slots) per split, below
-  // which the per-split merge dominates; no more splits than needed to give the
-  // 256 CUs about 1024 blocks.
+  // About one block per CU (256): a split block streams at the rate its
+  // instruction issue allows, and more, shorter splits add merge work without
+  // adding bandwidth (cold sweep at 16 q / 8 kv heads, L 4096 and 32768). At
+  // least 64 slots per split below that, where the per-split merge dominates.
   const int by_len = (cap + 63) / 64;
-  int by_grid = (1024 + B * Hkv - 1) / (B * Hkv);
+  int by_grid = (256 + B * Hkv - 1) / (B * Hkv);
   if (by_grid < 1) by_grid = 1;
   int n = by_len < by_grid ? by_len : by_grid;
   if (n > 256) n = 256;

@@ -151,8 +151,8 @@ constexpr int kMergeInGemvMaxSplits = 16;
 // wavefront of the block multiplies), once per block:
 //   kXRow, NORM: h = bf16(w * bf16(x * rsqrt(mean x^2 + eps)))   (x from a row or table[token])
 //   kXRow:       h = x
-//   kXMerge:     h = bf16(sum_s w_s acc_s / sum_s w_s l_s), the split-K merge with
-//                attn_combine_one's arithmetic, K / head_dim heads
+//   kXMerge:     h = bf16(sum_s w_s acc_s / sum_s w_s l_s), w_s = exp(m_s - max m),
+//                the split-K merge over K / head_dim heads, splits in order
 // Each thread owns 8 consecutive elements per pass. The loads are issued by
 // stage_load() BEFORE the kernel's weight loads: vector loads retire in order,
 // so the activation can then be used without waiting for the weight stream.
@@ -469,8 +469,9 @@ __device__ __forceinline__ void head_norm_rope(const u32x4 xr, const u32x4 wr, c
 // other block of the launch touches slot p, so no barrier orders the store.
 template <int D, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep a) {
-  constexpr int EPL = AttnGeom<__bf16, D>::EPL;
-  constexpr int LPS = AttnGeom<__bf16, D>::LPS;
+  using Geo = AttnGeom<__bf16, D, kAttnThreads, 1, 4>;
+  constexpr int EPL = Geo::EPL;
+  constexpr int LPS = Geo::LPS;
   const int tid = threadIdx.x;
   const int d0 = (tid % LPS) * EPL;
   const int hk = blockIdx.x;
@@ -497,8 +498,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
 
   uint16_t* kc = a.k_cache + (int64_t)hk * a.c_sh;
   uint16_t* vc = a.v_cache + (int64_t)hk * a.c_sh;
-  AttnPipe pp;
-  attn_begin<__bf16, D>(pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached);
+  AttnPipe<1, 4> pp;
+  attn_begin<Geo>(pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached);
 
   float qf[G][EPL];
 #pragma unroll
@@ -517,20 +518,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
     }
   }
 
-  attn_partial<__bf16, D, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
+  attn_partial<Geo, __bf16, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
                              a.scale, a.ws_m, a.ws_l, a.ws_acc, (int64_t)(hk * G) * a.nsplit + split, a.nsplit,
                              owner ? kn : nullptr, owner ? vn : nullptr);
 }
 
-// Merge of the split partials: one block per query head, one thread per element.
+// Merge of the split partials: one block per query head.
+constexpr int kMergeThreads = 256;
+
 template <int D>
-__global__ __launch_bounds__(D) void attn_merge_kernel(const float* __restrict__ ws_m, const float* __restrict__ ws_l,
-                                                       const float* __restrict__ ws_acc, uint16_t* __restrict__ out,
-                                                       int nsplit) {
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict__ ws_m,
+                                                                   const float* __restrict__ ws_l,
+                                                                   const float* __restrict__ ws_acc,
+                                                                   uint16_t* __restrict__ out, int nsplit) {
   const int h = blockIdx.x;
-  const int d = threadIdx.x;
-  out[(int64_t)h * D + d] = f32_to_bf16(attn_combine_one(ws_m + (int64_t)h * nsplit, ws_l + (int64_t)h * nsplit,
-                                                         ws_acc + (int64_t)h * nsplit * D, nsplit, D, d));
+  float r;
+  if (attn_combine_block<D, kMergeThreads>(ws_m + (int64_t)h * nsplit, ws_l + (int64_t)h * nsplit,
+                                           ws_acc + (int64_t)h * nsplit * D, nsplit, r))
+    out[(int64_t)h * D + threadIdx.x] = f32_to_bf16(r);
 }
 
 // ------------------------------------------------------------------ host side
@@ -657,8 +662,8 @@ int launch_attn_step(const AttnStep& a, int G, uint16_t* out, bool merge, hipStr
   }
   if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
   if (merge)
-    hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((unsigned)(a.Hkv * G)), dim3(D), 0, st, a.ws_m, a.ws_l,
-                       a.ws_acc, out, a.nsplit);
+    hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((unsigned)(a.Hkv * G)), dim3(kMergeThreads), 0, st, a.ws_m,
+                       a.ws_l, a.ws_acc, out, a.nsplit);
   return EGPT_LAUNCH_STATUS();
 }
 
