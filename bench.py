@@ -112,6 +112,21 @@ def gemv_roofline(eng, reps=20):
                      f'o_proj, gate/up, down) + lm_head {head.N}x{head.K}'}
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, 'profiles', 'fused_gemv_traffic_qwen3_1p7b.md')
+
+
+def measured_traffic(model):
+    """HBM bytes per fused-GEMV launch of the Qwen3-1.7B step, from the two calibrated rocprofv3 --pmc runs
+    (FETCH_SIZE, WRITE_SIZE) summarised in profiles/; None for other workloads or without the summary."""
+    if model != 'qwen3-1.7b' or not os.path.isfile(TRAFFIC_SUMMARY):
+        return None
+    with open(TRAFFIC_SUMMARY) as f:
+        for line in f:
+            if line.startswith('traffic_bytes_per_launch:'):
+                return int(line.split(':', 1)[1])
+    return None
+
+
 def attention_roofline(L=32768, hq=16, hkv=8, d=128, copies=4, reps=5):
     """Split-K GQA decode attention over all L slots, rotating `copies` K/V sets (> 512 MB)."""
     from efficientgpt_amd import _lib
@@ -246,6 +261,10 @@ def main():
         mean_len = args.prompt + args.warmup + (args.steps + 1) / 2
 
         roof = gemv_roofline(eng)
+        roof['traffic'] = measured_traffic(args.model)
+        if roof['traffic'] is not None:
+            roof['traffic_source'] = ('rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of bench.py, scaled by a 1 GiB copy: '
+                                      'profiles/fused_gemv_traffic_qwen3_1p7b.md')
 
         stream = None
         gpu_tokens = []
