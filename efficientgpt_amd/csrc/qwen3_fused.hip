@@ -156,16 +156,16 @@ constexpr int kMergeInGemvMaxSplits = 16;
 // Each thread owns 8 consecutive elements per pass. The loads are issued by
 // stage_load() BEFORE the kernel's weight loads: vector loads retire in order,
 // so the activation can then be used without waiting for the weight stream.
-template <int NTHREADS>
+template <int NTHREADS, int NCH>
 struct Staged {
-  static constexpr int kPasses = (kMaxChunks * kFChunk + NTHREADS * 8 - 1) / (NTHREADS * 8);
+  static constexpr int kPasses = (NCH * kFChunk + NTHREADS * 8 - 1) / (NTHREADS * 8);
   u32x4 xv[kPasses], nv[kPasses];
   float mv[kMergeInGemvMaxSplits], lv[kMergeInGemvMaxSplits];
   u32x4 lo[kMergeInGemvMaxSplits], hi[kMergeInGemvMaxSplits];
 };
 
-template <int NTHREADS, bool NORM, int XSRC>
-__device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS>& st) {
+template <int NTHREADS, int NCH, bool NORM, int XSRC>
+__device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS, NCH>& st) {
   const int tid = threadIdx.x;
   const u32x4 z{0u, 0u, 0u, 0u};
   if constexpr (XSRC == kXMerge) {
@@ -189,7 +189,7 @@ __device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS>&
   } else {
     const uint16_t* xr = token_row(a.x, a.x_token, a.x_ld, a.x_rows);
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
       const bool in = k8 < a.K;
       st.xv[p] = in ? ld16(xr + k8) : z;
@@ -198,8 +198,8 @@ __device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS>&
   }
 }
 
-template <int NTHREADS, bool NORM, int XSRC>
-__device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NTHREADS>& st, uint16_t* hs) {
+template <int NTHREADS, int NCH, bool NORM, int XSRC>
+__device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NTHREADS, NCH>& st, uint16_t* hs) {
   const int tid = threadIdx.x;
   if constexpr (XSRC == kXMerge) {
     const int k8 = tid * 8;
@@ -231,7 +231,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
     __shared__ float red[NTHREADS / kWave];
     float ss = 0.f;
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
       float v[8];
       Elem<__bf16>::unpack(st.xv[p], v);
 #pragma unroll
@@ -245,7 +245,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
     for (int j = 0; j < NTHREADS / kWave; ++j) total += red[j];
     const float inv = rsqrtf(total / (float)a.K + a.eps);
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
       if (k8 < a.K) {
         float v[8], w[8];
@@ -261,7 +261,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
     }
   } else {
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
       if (k8 < a.K) *(u32x4*)(hs + k8) = st.xv[p];
     }
@@ -269,49 +269,76 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
   lds_barrier();
 }
 
-// Weight rows of wave tile t (RH output features; SwiGLU: RH gate rows then the
-// RH matching up rows) and the epilogue operands of the feature lane j < RH
-// stores. Rows past N are clamped to N - 1 and never stored.
-template <int R, int NCH, int EPI>
-struct GemvTile {
-  static constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
-  u32x4 w[NCH][R];
-  float sc, sc_up, res;
+// Weight rows of wave tile t: RH output features; SwiGLU: RH gate rows then the
+// RH matching up rows. Rows past N are clamped to N - 1 and never stored.
+template <int R, int EPI>
+__device__ __forceinline__ void tile_rows(const FusedGemv& a, int64_t t, const int8_t* (&rows)[R]) {
+  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
+  const int64_t f0 = t * RH;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t fr = min(f0 + (r % RH), (int64_t)a.N - 1);
+    rows[r] = a.w + ((EPI == kEpiSwiGLU && r >= RH) ? fr + a.N : fr) * a.ldw;
+  }
+}
 
-  __device__ __forceinline__ void load(const FusedGemv& a, int64_t t, int lane) {
-    const int64_t f0 = t * RH;
+// Epilogue operands of the feature lane j < RH stores in tile t.
+struct GemvEpi {
+  float sc, sc_up, res;
+};
+
+template <int R, int EPI>
+__device__ __forceinline__ GemvEpi tile_epi(const FusedGemv& a, int64_t t, int lane) {
+  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
+  const int64_t fc = min(t * RH + (lane < RH ? lane : 0), (int64_t)a.N - 1);
+  GemvEpi e;
+  e.sc = a.scale[fc];
+  e.sc_up = EPI == kEpiSwiGLU ? a.scale[a.N + fc] : 0.f;
+  e.res = EPI == kEpiResid ? bf16_to_f32(token_row(a.resid, a.resid_token, a.resid_ld, a.x_rows)[fc]) : 0.f;
+  return e;
+}
+
+// CG chunks (1 KiB each) of R weight rows, in registers.
+template <int R, int CG>
+struct GemvStage {
+  u32x4 w[CG][R];
+
+  __device__ __forceinline__ void load(const FusedGemv& a, const int8_t* const (&rows)[R], int c0, int lane) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t fr = min(f0 + (r % RH), (int64_t)a.N - 1);
-      const int8_t* row = a.w + ((EPI == kEpiSwiGLU && r >= RH) ? fr + a.N : fr) * a.ldw;
+    for (int c = 0; c < CG; ++c) {
+      const int k = (c0 + c) * kFChunk + lane * 16;
+      const bool kin = k < a.K;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int k = c * kFChunk + lane * 16;
-        w[c][r] = k < a.K ? ld16_stream(row + k) : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int r = 0; r < R; ++r) w[c][r] = kin ? ld16_stream(rows[r] + k) : u32x4{0u, 0u, 0u, 0u};
     }
-    const int64_t fc = min(f0 + (lane < RH ? lane : 0), (int64_t)a.N - 1);
-    sc = a.scale[fc];
-    sc_up = EPI == kEpiSwiGLU ? a.scale[a.N + fc] : 0.f;
-    res = EPI == kEpiResid ? bf16_to_f32(token_row(a.resid, a.resid_token, a.resid_ld, a.x_rows)[fc]) : 0.f;
   }
 };
+
+// Chunks per register stage: all of a row up to 4 KiB, else 3 or 4 chunks, so
+// at most two stages (8 x R 16-byte loads per lane) are live at a time.
+template <int NCH>
+constexpr int kStageChunks = NCH <= 4 ? NCH : (NCH % 4 == 0 ? 4 : 3);
 
 // One int8 GEMV of a single activation row with a fused prologue / epilogue.
 // A block is W wavefronts. A wavefront owns RH output features per tile (R
 // weight rows: SwiGLU pairs each gate row with its up row) and walks tiles
 // t, t + stride, ... (one tile per wavefront unless the grid is capped, as for
-// the lm_head), streaming each tile's rows with 16-byte non-temporal loads and
-// prefetching the next tile's rows while it multiplies the current one. The
-// activation is staged once per block in LDS (stage_activation), its loads
-// issued before the weights: vector loads retire in order. LDS hand-offs use
-// lds_barrier(), which does not wait for the weight stream. Argmax: each lane
-// keeps its best (value, index) across tiles; the block reduces once.
+// the lm_head). Rows stream with 16-byte non-temporal loads in stages of CG
+// chunks, double-buffered: the next stage (or the next tile's first stage) is
+// issued before the current one is multiplied, so long rows (K = 12288) keep
+// the same registers as short ones. The activation is staged once per block in
+// LDS (stage_load / stage_finish), its loads issued before the weights: vector
+// loads retire in order. LDS hand-offs use lds_barrier(), which does not wait
+// for the weight stream. Argmax: each lane keeps its best (value, index)
+// across tiles; the block reduces once.
 template <int R, int NCH, int EPI, bool NORM, int XSRC, int W>
 __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a) {
-  using Tile = GemvTile<R, NCH, EPI>;
-  constexpr int RH = Tile::RH;
+  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
+  constexpr int CG = kStageChunks<NCH>;
+  constexpr int NST = NCH / CG;
+  static_assert(NCH % CG == 0, "chunk stages must tile the row");
   static_assert(EPI != kEpiSwiGLU || R % 2 == 0, "SwiGLU pairs rows");
+  using Stage = GemvStage<R, CG>;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int64_t ntiles = (a.N + RH - 1) / RH;
@@ -319,42 +346,59 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
   int64_t t = (int64_t)blockIdx.x * W + wave;
 
   // Activation loads first (they retire first), then the weight stream.
-  Staged<W * kWave> stg;
-  stage_load<W * kWave, NORM, XSRC>(a, stg);
-  Tile cur;
-  cur.load(a, t, lane);
+  Staged<W * kWave, NCH> stg;
+  stage_load<W * kWave, NCH, NORM, XSRC>(a, stg);
+  const int8_t* rows[R];
+  tile_rows<R, EPI>(a, t, rows);
+  Stage cur;
+  cur.load(a, rows, 0, lane);
+  GemvEpi ep = tile_epi<R, EPI>(a, t, lane);
   __shared__ __align__(16) uint16_t hs[NCH * kFChunk];
-  stage_finish<W * kWave, NORM, XSRC>(a, stg, hs);
+  stage_finish<W * kWave, NCH, NORM, XSRC>(a, stg, hs);
 
-  // Only the capped lm_head grid walks several tiles per wavefront; the other
-  // launches give every wavefront one tile, so they keep no second buffer.
+  // Only the capped lm_head grid walks several tiles per wavefront.
   constexpr bool kMulti = EPI == kEpiArgmax;
   ArgBest best{-INFINITY, 0x7fffffff};
   for (; t < ntiles; t += stride) {
     const bool more = kMulti && t + stride < ntiles;
-    Tile nxt;
-    if (more) nxt.load(a, t + stride, lane);
+    const int8_t* nrows[R];
+    GemvEpi nep = ep;
+    if (more) tile_rows<R, EPI>(a, t + stride, nrows);
 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
     float sx = 0.f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int k = c * kFChunk + lane * 16;
-      float xf[16];
-      if (k < a.K) {
-        unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) xf[e] = 0.f;
+    // Not unrolled: unrolled, the scheduler hoists every stage's loads to the
+    // top and all NST stages stay live (spills at K = 12288).
+#pragma unroll 1
+    for (int st = 0; st < NST; ++st) {
+      Stage nxt;
+      const bool next_stage = st + 1 < NST;
+      if (next_stage) {
+        nxt.load(a, rows, (st + 1) * CG, lane);
+      } else if (more) {
+        nxt.load(a, nrows, 0, lane);
+        nep = tile_epi<R, EPI>(a, t + stride, lane);
       }
-      float ts = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) ts += xf[e];
-      sx += ts;
+      for (int c = 0; c < CG; ++c) {
+        const int k = (st * CG + c) * kFChunk + lane * 16;
+        float xf[16];
+        if (k < a.K) {
+          unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
+        } else {
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xf, acc[r]);
+          for (int e = 0; e < 16; ++e) xf[e] = 0.f;
+        }
+        float ts = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ts += xf[e];
+        sx += ts;
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xf, acc[r]);
+      }
+      if (next_stage || more) cur = nxt;
     }
 
     // Row totals (wave-uniform); lane j < RH keeps feature t * RH + j.
@@ -371,24 +415,28 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
     const int64_t f = t * RH + lane;
     const bool own = lane < RH && f < a.N;
     if constexpr (EPI == kEpiStore) {
-      if (own) a.y[f] = f32_to_bf16(mine * cur.sc);
+      if (own) a.y[f] = f32_to_bf16(mine * ep.sc);
     } else if constexpr (EPI == kEpiResid) {
-      if (own) a.y[f] = f32_to_bf16(cur.res + bf16r(mine * cur.sc));
+      if (own) a.y[f] = f32_to_bf16(ep.res + bf16r(mine * ep.sc));
     } else if constexpr (EPI == kEpiSwiGLU) {
       if (own) {
-        const float g = bf16r(mine * cur.sc);
-        const float u = bf16r(mine_up * cur.sc_up);
+        const float g = bf16r(mine * ep.sc);
+        const float u = bf16r(mine_up * ep.sc_up);
         const float sg = bf16r(g / (1.0f + expf(-g)));
         a.y[f] = f32_to_bf16(sg * u);
       }
     } else {
       if (own) {
-        const uint16_t lg = f32_to_bf16(mine * cur.sc);
+        const uint16_t lg = f32_to_bf16(mine * ep.sc);
         if (a.y) a.y[f] = lg;
         best = arg_better(best, ArgBest{bf16_to_f32(lg), (int)f});
       }
     }
-    if (more) cur = nxt;
+    if (more) {
+      ep = nep;
+#pragma unroll
+      for (int r = 0; r < R; ++r) rows[r] = nrows[r];
+    }
   }
 
   if constexpr (EPI == kEpiArgmax) {  // per-block maximum of the logits

@@ -35,6 +35,9 @@ import torch
 from . import _lib
 from .int8_linear import MAX_DECODE_ROWS, quantize_weight
 
+# Prompts longer than this take the library-GEMM attention in prefill.
+PREFILL_KERNEL_MAX_ROWS = 64
+
 LINEARS = ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj', 'self_attn.o_proj',
            'mlp.gate_proj', 'mlp.up_proj', 'mlp.down_proj')
 
@@ -266,7 +269,7 @@ class Qwen3Int8Engine:
         else:
             out[:rows] = ((x[:rows] @ q.to(torch.bfloat16).t()).float() * s).to(torch.bfloat16)
 
-    def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first):
+    def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first, pos0=0):
         lib, c, L, st = _lib.lib(), self.cfg, self.layers[i], self._stream()
         d = c.head_dim
         if first:
@@ -282,7 +285,23 @@ class Qwen3Int8Engine:
             qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), L['qn_w'].data_ptr(), L['kn_w'].data_ptr(),
             self.cos.data_ptr(), self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(),
             kc.stride(0), kc.stride(1), rows, c.heads, c.kv_heads, d, self.cap, c.rms_eps, st))
-        # attention: every query row is a batch row over the shared cache (batch stride 0)
+        if rows > PREFILL_KERNEL_MAX_ROWS:
+            self._prefill_attention(qrot, kc, vc, rows, pos0, attn)
+        else:
+            self._kernel_attention(qrot, kc, vc, rows, positions, pos_stride, attn)
+        self._linear(attn, L['o_q'], L['o_s'], o, rows)
+        _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
+            x.data_ptr(), x.stride(0), o.data_ptr(), o.stride(0), L['post_w'].data_ptr(), h.data_ptr(), h.stride(0),
+            rows, c.hidden, c.rms_eps, st))
+        self._linear(h, L['gu_q'], L['gu_s'], gu, rows)
+        _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
+                                                      act.stride(0), rows, st))
+        self._linear(act, L['down_q'], L['down_s'], down, rows)
+
+    def _kernel_attention(self, qrot, kc, vc, rows, positions, pos_stride, attn):
+        """Split-K attention of `rows` query rows over the shared cache (each row a batch row, batch stride 0)."""
+        lib, c, st = _lib.lib(), self.cfg, self._stream()
+        d = c.head_dim
         if rows == 1:
             nsplit, ws = self.nsplit, self.attn_ws
         else:
@@ -298,14 +317,26 @@ class Qwen3Int8Engine:
             positions.data_ptr(), pos_stride,
             attn.data_ptr(), attn.stride(0), d,
             ws.data_ptr(), ws.numel(), rows, c.heads, c.kv_heads, self.cap, d, nsplit, d ** -0.5, st))
-        self._linear(attn, L['o_q'], L['o_s'], o, rows)
-        _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
-            x.data_ptr(), x.stride(0), o.data_ptr(), o.stride(0), L['post_w'].data_ptr(), h.data_ptr(), h.stride(0),
-            rows, c.hidden, c.rms_eps, st))
-        self._linear(h, L['gu_q'], L['gu_s'], gu, rows)
-        _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
-                                                      act.stride(0), rows, st))
-        self._linear(act, L['down_q'], L['down_s'], down, rows)
+
+    @torch.inference_mode()
+    def _prefill_attention(self, qrot, kc, vc, rows, pos0, attn, chunk=1024):
+        """Causal attention of a long prompt in fp32 on the library GEMM (the decode kernel would rescan the
+        prefix once per query row). Query t at position pos0 + t attends to slots 0..pos0 + t."""
+        c = self.cfg
+        d, g = c.head_dim, c.heads // c.kv_heads
+        n = pos0 + rows
+        kt = kc[:, :n].float().transpose(1, 2).contiguous()  # [Hkv, D, n]
+        v = vc[:, :n].float().contiguous()  # [Hkv, n, D]
+        slots = torch.arange(n, device=self.device)
+        for r0 in range(0, rows, chunk):
+            r1 = min(rows, r0 + chunk)
+            cr = r1 - r0
+            q = qrot[r0:r1].view(cr, c.kv_heads, g, d).permute(1, 2, 0, 3).reshape(c.kv_heads, g * cr, d).float()
+            s = torch.matmul(q.contiguous(), kt) * (d ** -0.5)  # [Hkv, g*cr, n]
+            qpos = (pos0 + r0 + torch.arange(cr, device=self.device)).repeat(g)
+            s.masked_fill_(slots[None, None, :] > qpos[None, :, None], float('-inf'))
+            o = torch.matmul(torch.softmax(s, dim=-1), v)  # [Hkv, g*cr, D]
+            attn[r0:r1] = o.view(c.kv_heads, g, cr, d).permute(2, 0, 1, 3).reshape(cr, c.heads * d).to(attn.dtype)
 
     def _head(self, x, down, h):
         """Final residual add + norm of one row, lm_head GEMV, argmax into token, position += 1."""
@@ -373,7 +404,7 @@ class Qwen3Int8Engine:
         _lib.check('egpt_embed', lib.egpt_embed(ids.data_ptr(), t, self.embed.data_ptr(), self.embed.stride(0),
                                                 c.vocab, x.data_ptr(), x.stride(0), c.hidden, self._stream()))
         for i in range(c.layers):
-            self._layer(i, t, x, h, qkv, qrot, attn, o, gu, act, down, positions, 1, first=(i == 0))
+            self._layer(i, t, x, h, qkv, qrot, attn, o, gu, act, down, positions, 1, first=(i == 0), pos0=pos0)
         self.position.fill_(pos0 + t - 1)  # argmax advances it to pos0 + t
         self._head(x[t - 1:], down[t - 1:], h[t - 1:])
         return self.logits[0]

@@ -46,9 +46,9 @@ def oracle_greedy_with_margins(orc, prompt, n):
 
 @pytest.mark.parametrize('shape,std', [(TINY, 0.2), (SMALL, 0.15)])
 def test_prefill_logits_match_oracle(shape, std):
-    eng, orc = build(shape, seed=1, std=std, cap=96)
+    eng, orc = build(shape, seed=1, std=std, cap=160)
     g = torch.Generator().manual_seed(2)
-    for p in (1, 5, 17, 37):
+    for p in (1, 5, 17, 37, 100):  # 100 rows: the long-prompt attention path
         prompt = torch.randint(0, shape.vocab, (p,), generator=g)
         eng.reset()
         got = eng.prefill(prompt).float().cpu()
