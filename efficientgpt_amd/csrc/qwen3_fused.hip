@@ -356,8 +356,26 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
   __shared__ __align__(16) uint16_t hs[NCH * kFChunk];
   stage_finish<W * kWave, NCH, NORM, XSRC>(a, stg, hs);
 
-  // Only the capped lm_head grid walks several tiles per wavefront.
+  // Only the capped lm_head grid walks several tiles per wavefront; it keeps
+  // its activation chunks (and their sum) in registers across tiles.
   constexpr bool kMulti = EPI == kEpiArgmax;
+  constexpr bool kHoistX = kMulti && NST == 1;
+  float xh[kHoistX ? CG : 1][16];
+  float sxh = 0.f;
+  if constexpr (kHoistX) {
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const int k = c * kFChunk + lane * 16;
+      if (k < a.K) {
+        unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xh[c]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xh[c][e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sxh += xh[c][e];
+    }
+  }
   ArgBest best{-INFINITY, 0x7fffffff};
   for (; t < ntiles; t += stride) {
     const bool more = kMulti && t + stride < ntiles;
@@ -381,22 +399,30 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
         nxt.load(a, nrows, 0, lane);
         nep = tile_epi<R, EPI>(a, t + stride, lane);
       }
+      if constexpr (kHoistX) {
 #pragma unroll
-      for (int c = 0; c < CG; ++c) {
-        const int k = (st * CG + c) * kFChunk + lane * 16;
-        float xf[16];
-        if (k < a.K) {
-          unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
-        } else {
+        for (int c = 0; c < CG; ++c)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) xf[e] = 0.f;
+          for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xh[c], acc[r]);
+        sx = sxh;
+      } else {
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+          const int k = (st * CG + c) * kFChunk + lane * 16;
+          float xf[16];
+          if (k < a.K) {
+            unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xf[e] = 0.f;
+          }
+          float ts = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) ts += xf[e];
+          sx += ts;
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xf, acc[r]);
         }
-        float ts = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) ts += xf[e];
-        sx += ts;
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xf, acc[r]);
       }
       if (next_stage || more) cur = nxt;
     }
