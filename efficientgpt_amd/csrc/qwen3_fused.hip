@@ -153,7 +153,8 @@ constexpr int kMergeInGemvMaxSplits = 16;
 //   kXRow:       h = x
 //   kXMerge:     h = bf16(sum_s w_s acc_s / sum_s w_s l_s), w_s = exp(m_s - max m),
 //                the split-K merge over K / head_dim heads, splits in order
-// Each thread owns 8 consecutive elements per pass. The loads are issued by
+// Each thread owns 8 consecutive elements per pass; elements from K up to the
+// end of the last 1 KiB chunk are stored as 0. The loads are issued by
 // stage_load() BEFORE the kernel's weight loads: vector loads retire in order,
 // so the activation can then be used without waiting for the weight stream.
 template <int NTHREADS, int NCH>
@@ -203,7 +204,9 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
   const int tid = threadIdx.x;
   if constexpr (XSRC == kXMerge) {
     const int k8 = tid * 8;
-    if (k8 < a.K) {
+    if (k8 >= a.K) {
+      if (k8 < NCH * kFChunk) *(u32x4*)(hs + k8) = u32x4{0u, 0u, 0u, 0u};
+    } else {
       float mx = -INFINITY;
 #pragma unroll
       for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) mx = fmaxf(mx, st.mv[sp]);
@@ -247,7 +250,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
 #pragma unroll
     for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
-      if (k8 < a.K) {
+      if (k8 < NCH * kFChunk) {  // past K, x and w load as 0 and h is 0
         float v[8], w[8];
         Elem<__bf16>::unpack(st.xv[p], v);
         Elem<__bf16>::unpack(st.nv[p], w);
@@ -263,7 +266,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
 #pragma unroll
     for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
-      if (k8 < a.K) *(u32x4*)(hs + k8) = st.xv[p];
+      if (k8 < NCH * kFChunk) *(u32x4*)(hs + k8) = st.xv[p];  // 0 past K
     }
   }
   lds_barrier();
@@ -298,7 +301,12 @@ __device__ __forceinline__ GemvEpi tile_epi(const FusedGemv& a, int64_t t, int l
   return e;
 }
 
-// CG chunks (1 KiB each) of R weight rows, in registers.
+// CG chunks (1 KiB each) of R weight rows, in registers. Every lane loads:
+// a lane past K (K is a multiple of 16) reads column 0 instead, and its
+// activation values are zero, so those weights add exactly 0. Unconditional
+// loads keep the wait counts exact (a guarded load would be a branch, and the
+// compiler's vmcnt before the activation's LDS store would then wait for the
+// whole weight stage).
 template <int R, int CG>
 struct GemvStage {
   u32x4 w[CG][R];
@@ -307,38 +315,99 @@ struct GemvStage {
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
       const int k = (c0 + c) * kFChunk + lane * 16;
-      const bool kin = k < a.K;
+      const int kl = k < a.K ? k : 0;
 #pragma unroll
-      for (int r = 0; r < R; ++r) w[c][r] = kin ? ld16_stream(rows[r] + k) : u32x4{0u, 0u, 0u, 0u};
+      for (int r = 0; r < R; ++r) w[c][r] = ld16_stream(rows[r] + kl);
     }
   }
 };
 
-// Chunks per register stage: all of a row up to 4 KiB, else 3 or 4 chunks, so
-// at most two stages (8 x R 16-byte loads per lane) are live at a time.
-template <int NCH>
-constexpr int kStageChunks = NCH <= 4 ? NCH : (NCH % 4 == 0 ? 4 : 3);
+// Chunks per register stage: the largest divisor of NCH with at most 8 16-byte
+// loads per lane (32 VGPRs) per stage; two stages are live at a time.
+constexpr int stage_chunks(int R, int NCH) {
+  int cg = NCH;
+  while (cg > 1 && (R * cg > 8 || NCH % cg)) --cg;
+  return cg;
+}
+
+// acc[r] += sum over the CG chunks of stage s (first chunk c0) of w * x, biased
+// form; sx += sum of x. Columns past K have x = 0 in LDS.
+template <int R, int CG>
+__device__ __forceinline__ void stage_mac(const GemvStage<R, CG>& s, const uint16_t* hs, int c0, int lane,
+                                          float (&acc)[R], float& sx) {
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int k = (c0 + c) * kFChunk + lane * 16;
+    float xf[16];
+    unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
+    float ts = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ts += xf[e];
+    sx += ts;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = dot16_biased(s.w[c][r], xf, acc[r]);
+  }
+}
+
+// Row totals of tile t (wave-uniform) and the epilogue: lane j < RH stores
+// feature t * RH + j. Argmax keeps the lane's best (value, index) in best.
+template <int R, int EPI>
+__device__ __forceinline__ void tile_finish(const FusedGemv& a, int64_t t, int lane, const float (&acc)[R], float sx,
+                                            const GemvEpi& ep, ArgBest& best) {
+  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
+  float mine = 0.f, mine_up = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v = wave_sum(acc[r] - 128.f * sx);
+    if (r < RH) {
+      if (lane == r) mine = v;
+    } else {
+      if (lane == r - RH) mine_up = v;
+    }
+  }
+  const int64_t f = t * RH + lane;
+  const bool own = lane < RH && f < a.N;
+  if constexpr (EPI == kEpiStore) {
+    if (own) a.y[f] = f32_to_bf16(mine * ep.sc);
+  } else if constexpr (EPI == kEpiResid) {
+    if (own) a.y[f] = f32_to_bf16(ep.res + bf16r(mine * ep.sc));
+  } else if constexpr (EPI == kEpiSwiGLU) {
+    if (own) {
+      const float g = bf16r(mine * ep.sc);
+      const float u = bf16r(mine_up * ep.sc_up);
+      const float sg = bf16r(g / (1.0f + expf(-g)));
+      a.y[f] = f32_to_bf16(sg * u);
+    }
+  } else {
+    if (own) {
+      const uint16_t lg = f32_to_bf16(mine * ep.sc);
+      if (a.y) a.y[f] = lg;
+      best = arg_better(best, ArgBest{bf16_to_f32(lg), (int)f});
+    }
+  }
+}
 
 // One int8 GEMV of a single activation row with a fused prologue / epilogue.
 // A block is W wavefronts. A wavefront owns RH output features per tile (R
-// weight rows: SwiGLU pairs each gate row with its up row) and walks tiles
-// t, t + stride, ... (one tile per wavefront unless the grid is capped, as for
-// the lm_head). Rows stream with 16-byte non-temporal loads in stages of CG
-// chunks, double-buffered: the next stage (or the next tile's first stage) is
-// issued before the current one is multiplied, so long rows (K = 12288) keep
-// the same registers as short ones. The activation is staged once per block in
+// weight rows: SwiGLU pairs each gate row with its up row): one tile per
+// wavefront, except the capped lm_head grid, which walks tiles t, t + stride,
+// ... Rows stream with 16-byte non-temporal loads in stages of CG chunks, in two
+// ping-pong register buffers: stage s + 1 is issued before stage s is
+// multiplied, and scheduling barriers keep the compiler from hoisting later
+// stages (all of a K = 12288 row would not fit in registers). No buffer is
+// copied, so the wait before each stage is for that stage alone. The activation is staged once per block in
 // LDS (stage_load / stage_finish), its loads issued before the weights: vector
 // loads retire in order. LDS hand-offs use lds_barrier(), which does not wait
 // for the weight stream. Argmax: each lane keeps its best (value, index)
 // across tiles; the block reduces once.
 template <int R, int NCH, int EPI, bool NORM, int XSRC, int W>
 __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a) {
-  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
-  constexpr int CG = kStageChunks<NCH>;
+  constexpr int CG = stage_chunks(R, NCH);
   constexpr int NST = NCH / CG;
-  static_assert(NCH % CG == 0, "chunk stages must tile the row");
+  constexpr bool kMulti = EPI == kEpiArgmax;
   static_assert(EPI != kEpiSwiGLU || R % 2 == 0, "SwiGLU pairs rows");
   using Stage = GemvStage<R, CG>;
+  constexpr int RH = EPI == kEpiSwiGLU ? R / 2 : R;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int64_t ntiles = (a.N + RH - 1) / RH;
@@ -350,122 +419,89 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
   stage_load<W * kWave, NCH, NORM, XSRC>(a, stg);
   const int8_t* rows[R];
   tile_rows<R, EPI>(a, t, rows);
-  Stage cur;
-  cur.load(a, rows, 0, lane);
+  Stage buf[2];
+  buf[0].load(a, rows, 0, lane);
   GemvEpi ep = tile_epi<R, EPI>(a, t, lane);
   __shared__ __align__(16) uint16_t hs[NCH * kFChunk];
   stage_finish<W * kWave, NCH, NORM, XSRC>(a, stg, hs);
 
-  // Only the capped lm_head grid walks several tiles per wavefront; it keeps
-  // its activation chunks (and their sum) in registers across tiles.
-  constexpr bool kMulti = EPI == kEpiArgmax;
-  constexpr bool kHoistX = kMulti && NST == 1;
-  float xh[kHoistX ? CG : 1][16];
-  float sxh = 0.f;
-  if constexpr (kHoistX) {
+  ArgBest best{-INFINITY, 0x7fffffff};
+  if constexpr (!kMulti || NST > 1) {
+    // Stages of a tile over the ping-pong buffers (stage 0 in buf[0]).
+    for (; t < ntiles; t += stride) {
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+      float sx = 0.f;
+      // Pairs of stages (A = buf[0], B = buf[1]) while two or more follow the
+      // pair, then a tail of one or two stages. All loads in the loop body are
+      // unconditional, so each wait covers exactly the stage about to be used.
+      int st = 0;
+#pragma unroll 1
+      for (; st + 2 < NST; st += 2) {
+        buf[1].load(a, rows, (st + 1) * CG, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_mac<R, CG>(buf[0], hs, st * CG, lane, acc, sx);
+        __builtin_amdgcn_sched_barrier(0);
+        buf[0].load(a, rows, (st + 2) * CG, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_mac<R, CG>(buf[1], hs, (st + 1) * CG, lane, acc, sx);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (NST % 2 == 0) {
+        buf[1].load(a, rows, (NST - 1) * CG, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_mac<R, CG>(buf[0], hs, (NST - 2) * CG, lane, acc, sx);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_mac<R, CG>(buf[1], hs, (NST - 1) * CG, lane, acc, sx);
+      } else {
+        stage_mac<R, CG>(buf[0], hs, (NST - 1) * CG, lane, acc, sx);
+      }
+      tile_finish<R, EPI>(a, t, lane, acc, sx, ep, best);
+      if (!kMulti || t + stride >= ntiles) break;
+      tile_rows<R, EPI>(a, t + stride, rows);
+      buf[0].load(a, rows, 0, lane);
+      ep = tile_epi<R, EPI>(a, t + stride, lane);
+    }
+  } else {
+    // One-stage rows over many tiles: the next tile's row is issued before this
+    // one is multiplied, and the activation chunks (and their sum) stay in
+    // registers across tiles.
+    float xh[CG][16];
+    float sxh = 0.f;
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
       const int k = c * kFChunk + lane * 16;
-      if (k < a.K) {
-        unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xh[c]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) xh[c][e] = 0.f;
-      }
+      unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xh[c]);
 #pragma unroll
       for (int e = 0; e < 16; ++e) sxh += xh[c][e];
     }
-  }
-  ArgBest best{-INFINITY, 0x7fffffff};
-  for (; t < ntiles; t += stride) {
-    const bool more = kMulti && t + stride < ntiles;
-    const int8_t* nrows[R];
-    GemvEpi nep = ep;
-    if (more) tile_rows<R, EPI>(a, t + stride, nrows);
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    float sx = 0.f;
-    // Not unrolled: unrolled, the scheduler hoists every stage's loads to the
-    // top and all NST stages stay live (spills at K = 12288).
-#pragma unroll 1
-    for (int st = 0; st < NST; ++st) {
+    Stage& cur = buf[0];
+    for (; t < ntiles; t += stride) {
+      const bool more = t + stride < ntiles;
+      const int8_t* nrows[R];
+      GemvEpi nep = ep;
       Stage nxt;
-      const bool next_stage = st + 1 < NST;
-      if (next_stage) {
-        nxt.load(a, rows, (st + 1) * CG, lane);
-      } else if (more) {
+      if (more) {
+        tile_rows<R, EPI>(a, t + stride, nrows);
         nxt.load(a, nrows, 0, lane);
         nep = tile_epi<R, EPI>(a, t + stride, lane);
       }
-      if constexpr (kHoistX) {
+      float acc[R];
 #pragma unroll
-        for (int c = 0; c < CG; ++c)
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
-          for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xh[c], acc[r]);
-        sx = sxh;
-      } else {
+      for (int c = 0; c < CG; ++c)
 #pragma unroll
-        for (int c = 0; c < CG; ++c) {
-          const int k = (st * CG + c) * kFChunk + lane * 16;
-          float xf[16];
-          if (k < a.K) {
-            unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) xf[e] = 0.f;
-          }
-          float ts = 0.f;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) ts += xf[e];
-          sx += ts;
-#pragma unroll
-          for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xf, acc[r]);
-        }
+        for (int r = 0; r < R; ++r) acc[r] = dot16_biased(cur.w[c][r], xh[c], acc[r]);
+      tile_finish<R, EPI>(a, t, lane, acc, sxh, ep, best);
+      if (more) {
+        cur = nxt;
+        ep = nep;
       }
-      if (next_stage || more) cur = nxt;
-    }
-
-    // Row totals (wave-uniform); lane j < RH keeps feature t * RH + j.
-    float mine = 0.f, mine_up = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(acc[r] - 128.f * sx);
-      if (r < RH) {
-        if (lane == r) mine = v;
-      } else {
-        if (lane == r - RH) mine_up = v;
-      }
-    }
-    const int64_t f = t * RH + lane;
-    const bool own = lane < RH && f < a.N;
-    if constexpr (EPI == kEpiStore) {
-      if (own) a.y[f] = f32_to_bf16(mine * ep.sc);
-    } else if constexpr (EPI == kEpiResid) {
-      if (own) a.y[f] = f32_to_bf16(ep.res + bf16r(mine * ep.sc));
-    } else if constexpr (EPI == kEpiSwiGLU) {
-      if (own) {
-        const float g = bf16r(mine * ep.sc);
-        const float u = bf16r(mine_up * ep.sc_up);
-        const float sg = bf16r(g / (1.0f + expf(-g)));
-        a.y[f] = f32_to_bf16(sg * u);
-      }
-    } else {
-      if (own) {
-        const uint16_t lg = f32_to_bf16(mine * ep.sc);
-        if (a.y) a.y[f] = lg;
-        best = arg_better(best, ArgBest{bf16_to_f32(lg), (int)f});
-      }
-    }
-    if (more) {
-      ep = nep;
-#pragma unroll
-      for (int r = 0; r < R; ++r) rows[r] = nrows[r];
     }
   }
-
-  if constexpr (EPI == kEpiArgmax) {  // per-block maximum of the logits
+  if constexpr (kMulti) {
     best = block_argbest<W>(best);
     if (threadIdx.x == 0) {
       a.part_v[blockIdx.x] = best.v;
