@@ -50,19 +50,22 @@ struct AttnGeom {
 template <typename T>
 constexpr bool kAttnDot2 = __is_same(T, __bf16);  // q . k on packed bf16 pairs
 
-// K/V rows in flight for one softmax stream (register double buffer).
+// K/V rows in flight for one softmax stream: U slots, LPR 16-byte loads each.
 template <int LPR, int U>
 struct AttnPipe {
   u32x4 kr[U][LPR], vr[U][LPR];
 };
 
+// Loads of one iteration of a stream: slots n0 + u * NG. Every lane loads, so
+// the wait counts stay exact: a slot at or past `end` reads slot 0 instead (in
+// bounds and live for any position), and attn_mac() masks it out.
 template <typename Geo, typename T, int LPR, int U>
 __device__ __forceinline__ void attn_issue(AttnPipe<LPR, U>& pp, const T* __restrict__ kb, int64_t k_sn,
-                                           const T* __restrict__ vb, int64_t v_sn, int64_t base, int64_t end) {
+                                           const T* __restrict__ vb, int64_t v_sn, int64_t n0, int64_t end) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t n = base + (int64_t)u * Geo::NG;
-    const int64_t nn = n < end ? n : base;  // never touch slots past the live range
+    const int64_t n = n0 + (int64_t)u * Geo::NG;
+    const int64_t nn = n < end ? n : 0;
 #pragma unroll
     for (int j = 0; j < LPR; ++j) {
       // K and V are read once per call: non-temporal loads stream them past
@@ -81,8 +84,7 @@ __device__ __forceinline__ void attn_begin(AttnPipe<LPR, U>& pp, const T* __rest
                                            const T* __restrict__ vbase, int64_t v_sn, int64_t start, int64_t end) {
   const int tid = threadIdx.x;
   const int d0 = (tid % Geo::LPS) * Geo::EPL;
-  const int64_t n0 = start + tid / Geo::LPS;
-  if (n0 < end) attn_issue<Geo>(pp, kbase + d0, k_sn, vbase + d0, v_sn, n0, end);
+  attn_issue<Geo>(pp, kbase + d0, k_sn, vbase + d0, v_sn, start + tid / Geo::LPS, end);
 }
 
 // Packed bf16 pairs of EPL fp32 values that are exact bf16 (queries, new keys).
@@ -118,6 +120,64 @@ __device__ __forceinline__ float attn_qk(const u32x4 (&kr)[LPR], const float (&q
     }
   }
   return p;
+}
+
+// One iteration of a softmax stream over the slots in pp (n0 + u * NG, those
+// before `end` valid): scores (q . k) * scale in fp32, online-softmax update of
+// (m, l, acc) for the G query heads.
+template <typename Geo, typename T, int G, int LPR, int U>
+__device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float (&qf)[G][Geo::EPL],
+                                         const uint32_t (&qp)[G][Geo::EPL / 2], int64_t n0, int64_t end, float scale,
+                                         float (&m)[G], float (&l)[G], float (&acc)[G][Geo::EPL]) {
+  constexpr int EPL = Geo::EPL;
+  constexpr int EPV = Geo::EPV;
+  constexpr int LPS = Geo::LPS;
+  constexpr int NG = Geo::NG;
+  bool valid[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) valid[u] = n0 + (int64_t)u * NG < end;
+  float s[U][G];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float p = group_sum<LPS>(attn_qk<Geo, T, LPR>(pp.kr[u], qf[g], qp[g])) * scale;
+      s[u][g] = valid[u] ? p : -INFINITY;  // the reference's fp32 logit: (q . k) * scale
+    }
+  }
+  float vf[U][EPL];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) {
+      Elem<T>::unpack(pp.vr[u][j], &vf[u][j * EPV]);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) vf[u][j * EPV + e] = valid[u] ? vf[u][j * EPV + e] : 0.f;
+    }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mt = m[g];
+#pragma unroll
+    for (int u = 0; u < U; ++u) mt = fmaxf(mt, s[u][g]);
+    if (mt == -INFINITY) continue;  // no valid slot yet in this stream
+    const float alpha = exp2f((m[g] - mt) * kLog2e);
+    float p[U];
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      p[u] = exp2f((s[u][g] - mt) * kLog2e);  // 0 for invalid slots
+      psum += p[u];
+    }
+    l[g] = l[g] * alpha + psum;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float a = acc[g][e] * alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) a = fmaf(p[u], vf[u][e], a);
+      acc[g][e] = a;
+    }
+    m[g] = mt;
+  }
 }
 
 // One block's partial softmax state over slots [start, end) of one kv head, for
@@ -164,58 +224,34 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
   }
 
   constexpr int64_t kStep = (int64_t)NG * U;  // slots one stream advances per iteration
-  // Register double buffer: the loads of iteration i+1 are issued before the
-  // arithmetic of iteration i.
-  for (int64_t n0 = start + grp; n0 < end; n0 += kStep) {
-    u32x4 kc[U][LPR], vc[U][LPR];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < LPR; ++j) {
-        kc[u][j] = pp.kr[u][j];
-        vc[u][j] = pp.vr[u][j];
-      }
-    if (n0 + kStep < end) attn_issue<Geo>(pp, kbase, k_sn, vbase, v_sn, n0 + kStep, end);
-
-    float s[U][G];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool valid = n0 + (int64_t)u * NG < end;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = group_sum<LPS>(attn_qk<Geo, T, LPR>(kc[u], qf[g], qp[g])) * scale;
-        s[u][g] = valid ? p : -INFINITY;  // the reference's fp32 logit: (q . k) * scale
-      }
-    }
-    float vf[U][EPL];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < LPR; ++j) Elem<T>::unpack(vc[u][j], &vf[u][j * EPV]);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mt = m[g];
-#pragma unroll
-      for (int u = 0; u < U; ++u) mt = fmaxf(mt, s[u][g]);
-      // slot n0 is always valid, so mt is finite
-      const float alpha = exp2f((m[g] - mt) * kLog2e);
-      float p[U];
-      float psum = 0.f;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        p[u] = exp2f((s[u][g] - mt) * kLog2e);  // 0 for invalid slots
-        psum += p[u];
-      }
-      l[g] = l[g] * alpha + psum;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        float a = acc[g][e] * alpha;
-#pragma unroll
-        for (int u = 0; u < U; ++u) a = fmaf(p[u], vf[u][e], a);
-        acc[g][e] = a;
-      }
-      m[g] = mt;
-    }
+  // Iterations are block-uniform: stream grp handles slots start + grp + i * NG.
+  // Two register buffers (pp = A, pb = B) in pairs of iterations: the loads of
+  // iteration i + 1 are issued before iteration i is computed, no buffer is
+  // copied, and all loads are unconditional, so each wait covers exactly the
+  // iteration about to be used while the next one stays in flight.
+  const int64_t n0 = start + grp;
+  const int64_t nit = end > start ? (end - start + kStep - 1) / kStep : 0;
+  AttnPipe<LPR, U> pb;
+  int64_t it = 0;
+#pragma unroll 1
+  for (; it + 2 < nit; it += 2) {
+    attn_issue<Geo>(pb, kbase, k_sn, vbase, v_sn, n0 + (it + 1) * kStep, end);
+    __builtin_amdgcn_sched_barrier(0);
+    attn_mac<Geo, T, G>(pp, qf, qp, n0 + it * kStep, end, scale, m, l, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    attn_issue<Geo>(pp, kbase, k_sn, vbase, v_sn, n0 + (it + 2) * kStep, end);
+    __builtin_amdgcn_sched_barrier(0);
+    attn_mac<Geo, T, G>(pb, qf, qp, n0 + (it + 1) * kStep, end, scale, m, l, acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (it + 1 < nit) {
+    attn_issue<Geo>(pb, kbase, k_sn, vbase, v_sn, n0 + (it + 1) * kStep, end);
+    __builtin_amdgcn_sched_barrier(0);
+    attn_mac<Geo, T, G>(pp, qf, qp, n0 + it * kStep, end, scale, m, l, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    attn_mac<Geo, T, G>(pb, qf, qp, n0 + (it + 1) * kStep, end, scale, m, l, acc);
+  } else if (it < nit) {
+    attn_mac<Geo, T, G>(pp, qf, qp, n0 + it * kStep, end, scale, m, l, acc);
   }
 
   if (xk) {  // block-uniform: the extra slot goes to stream 0

@@ -27,7 +27,7 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(
     const int64_t* __restrict__ position, int64_t pos_stride, float* __restrict__ ws_m, float* __restrict__ ws_l,
     float* __restrict__ ws_acc, int Hkv, int cap, int nsplit, float scale) {
   constexpr int LPR = kSplitLPR<T>;
-  constexpr int U = kSplitUnroll<T>;
+  constexpr int U = G >= 8 ? 2 : kSplitUnroll<T>;  // G >= 8: two buffers of 4 slots spill
   using Geo = AttnGeom<T, D, NT, LPR, U>;
   constexpr int EPL = Geo::EPL;
   constexpr int EPV = Geo::EPV;
