@@ -41,15 +41,6 @@ enum { kEpiStore = 0, kEpiResid = 1, kEpiSwiGLU = 2, kEpiArgmax = 3 };
 
 __device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
-// Workgroup barrier ordering LDS only. __syncthreads() also waits for every
-// outstanding global load of the wavefront (s_waitcnt vmcnt(0)), which would
-// stall the block behind its whole weight stream at each LDS hand-off.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 struct FusedGemv {
   const uint16_t* x;       // activation row, or a table when x_token is set
   const int64_t* x_token;  // device id selecting row x + token * x_ld (the embedding gather)

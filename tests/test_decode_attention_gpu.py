@@ -97,7 +97,7 @@ def test_split_count_invariance_and_single_pass():
     v = torch.randn(1, 8, 2048, 128, generator=g).cuda()
     pos = torch.tensor([1999], device='cuda')
     base = decode_attention_single_pass(q, k, v, pos)
-    for split in (16, 64, 256, 2048):
+    for split in (4, 16, 64, 256, 2048):  # 512, 128, 32, 8 and 1 splits
         other = decode_attention(q, k, v, pos, config=(split, 0, 0))
         assert float((other - base).abs().max()) < 1e-5
 
