@@ -29,6 +29,7 @@ Prints one JSON line:
 import argparse
 import ctypes
 import json
+import math
 import os
 import platform
 import sys
@@ -187,6 +188,13 @@ def host_threads():
     return len(os.sched_getaffinity(0)) or 1
 
 
+def near_tie_bound(top1):
+    """Greedy near-tie margin: the reference's 1e-2 on fp32 logits (research/phase5/benchmark_review.py:46),
+    or two bf16 ulps of the top logit when that is larger."""
+    a = abs(top1)
+    return max(1e-2, 2 * 2.0 ** (math.floor(math.log2(a)) - 7) if a > 0 else 0.0)
+
+
 def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
     """The CPU oracle on the same weights: prefill the prompt, then n_tokens greedy steps."""
     from oracle.qwen3 import Qwen3Oracle, Qwen3Shape
@@ -196,25 +204,37 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
                        c.rms_eps, c.tied)
     w = {k: v.cpu() for k, v in eng.weights.items()}
     orc = Qwen3Oracle(shape, w, dtype=torch.bfloat16, cap=len(prompt) + n_tokens + 1)
+    margins = []  # (top-1 - top-2, top-1) of the oracle's logits at each step
+
+    def pick(logits):
+        top2 = torch.topk(logits.float(), 2).values
+        margins.append((float(top2[0] - top2[1]), float(top2[0])))
+        return int(torch.argmax(logits))
+
     t0 = time.perf_counter()
-    logits = orc.forward(prompt, 0)
-    toks = [int(torch.argmax(logits))]
+    toks = [pick(orc.forward(prompt, 0))]
     t_first = time.perf_counter()
     pos = len(prompt)
     for _ in range(n_tokens - 1):
-        logits = orc.forward([toks[-1]], pos)
+        toks.append(pick(orc.forward([toks[-1]], pos)))
         pos += 1
-        toks.append(int(torch.argmax(logits)))
     t1 = time.perf_counter()
     decode_tps = (n_tokens - 1) / (t1 - t_first) if n_tokens > 1 else None
-    agree = sum(a == b for a, b in zip(toks, gpu_tokens[:n_tokens]))
+    gpu = list(gpu_tokens[:n_tokens])
+    first = next((i for i, (a, b) in enumerate(zip(toks, gpu)) if a != b), None)
+    agree = f'{n_tokens}/{n_tokens} identical'
+    if first is not None:  # free-running decodes: after a divergence the contexts differ
+        m, top = margins[first]
+        bound = near_tie_bound(top)
+        agree = (f'first {first}/{n_tokens} identical; at step {first} the oracle\'s top-1/top-2 margin is {m:.4g} '
+                 f'against the near-tie bound {bound:.4g} ({"a near-tie" if m < bound else "NOT a near-tie"})')
     return {'value': round(decode_tps, 3) if decode_tps else None, 'unit': 'tok/s', 'cores': torch.get_num_threads(),
             'kind': 'port',
             'sample': (f'CPU oracle (torch, bf16 activations, exact fp32 image of the int8 weights) on the same '
                        f'weights: prefill of the {len(prompt)}-token prompt ({t_first - t0:.1f} s), then '
                        f'{n_tokens} greedy tokens; decode tok/s = (n-1)/(decode time)'),
             'cpu': platform.processor() or platform.machine(),
-            'token_agreement_with_gpu': f'{agree}/{n_tokens}'}
+            'token_agreement_with_gpu': agree}
 
 
 def main():
