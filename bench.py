@@ -19,11 +19,14 @@ Prints one JSON line:
                   The set streams > 1.7 GB per pass, so it is HBM-cold by construction.
   attention       split-K decode attention at the largest context of the workload
                   family (16 q / 8 kv heads, D 128, L = 32768), rotating > 512 MB of K/V
+  attention_by_length  the same at L = 256 ... 16384
+  gemv_1x2048_6144     the reference's headline GEMV shape through egpt_int8_gemv, cold
   step            the whole step: weight + scale + KV bytes per token / ms per token
   copy_gbps       a device-to-device copy of 1 GiB, the measured bandwidth ceiling
   cpu_baseline    the CPU oracle (oracle/qwen3.py, torch on the host) on a bounded
                   sample of the same workload: prefill of the same prompt, then a few
-                  greedy decode steps, on the same weights
+                  greedy decode steps, on the same weights; `kernels` holds the
+                  reference's CPU forms of the GEMV and the attention timed on the host
 """
 
 import argparse
@@ -163,6 +166,78 @@ def attention_roofline(L=32768, hq=16, hkv=8, d=128, copies=4, reps=5):
             'kernel': 'attn_split_kernel + attn_combine_kernel (egpt_decode_attn), cold'}
 
 
+def gemv_cfg0(n=6144, k=2048, sets=48, reps=10):
+    """The reference's headline GEMV, one 2048-wide row times 6144 x 2048 int8 weights
+    (research/kernelagent/tasks.py:206-209), through egpt_int8_gemv over `sets` rotating weight
+    copies (> 512 MB) captured in one graph, so every call streams its weights from HBM."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device('cuda')
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+    ws = [torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8) for _ in range(sets)]
+    sc = torch.randn(n, generator=g, device=dev).abs() * 0.02 / 127
+    y = torch.empty(1, n, device=dev, dtype=torch.bfloat16)
+
+    def run():
+        st = _lib.stream_ptr()
+        for w in ws:
+            _lib.check('egpt_int8_gemv', lib.egpt_int8_gemv(x.data_ptr(), k, w.data_ptr(), k, sc.data_ptr(),
+                                                            y.data_ptr(), n, 1, n, k, st))
+
+    per_call = _time_graph(run, reps) / sets
+    nbytes = n * k + 4 * n + 2 * k + 2 * n
+    del ws
+    torch.cuda.empty_cache()
+    return {'bound': 'hbm', 'achieved': round(nbytes / per_call / 1e9, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+            'frac': round(nbytes / per_call / 1e9 / HBM_PEAK_GBPS, 4), 'shape': f'1x{k} -> {n}',
+            'bytes_per_call': nbytes, 'us_per_call': round(per_call * 1e6, 3),
+            'kernel': 'gemv_i8_rows (egpt_int8_gemv), cold, one call per weight copy'}
+
+
+def attention_sweep(lengths=(256, 1024, 4096, 16384)):
+    """attention_roofline at shorter live lengths, each over > 512 MB of rotating K/V copies."""
+    out = {}
+    for L in lengths:
+        r = attention_roofline(L=L, copies=max(4, (1 << 29) // (4096 * L) + 1), reps=3)
+        out[str(L)] = {k: r[k] for k in ('achieved', 'frac', 'nsplit', 'us_per_call')}
+    return out
+
+
+def cpu_kernels(threads):
+    """The reference's CPU-runnable forms of the two kernels on this host, beside the GPU figures:
+    the int8 linear's formula ((x @ W.bf16^T).float() * s).bf16 (research/realmodel/int8_linear.py:97)
+    at 1 x 2048 -> 6144, median of 20 calls; fp32 SDPA over 32768 slots, 16 q / 8 kv heads (the kv
+    heads repeated per group), median of 5 calls. Bytes are the kernels' algorithmic bytes."""
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    n, k = 6144, 2048
+    x = torch.randn(1, k, generator=g).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    sc = torch.randn(n, generator=g).abs() * 0.02 / 127
+
+    def timed(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return sorted(ts)[len(ts) // 2]
+
+    t_gemv = timed(lambda: ((x @ w.to(torch.bfloat16).t()).float() * sc).to(torch.bfloat16), 20)
+    hq, hkv, L, d = 16, 8, 32768, 128
+    q = torch.randn(1, hq, 1, d, generator=g)
+    kv = torch.randn(2, 1, hkv, L, d, generator=g).to(torch.bfloat16).float()
+    kk, vv = kv[0].repeat_interleave(hq // hkv, 1), kv[1].repeat_interleave(hq // hkv, 1)
+    t_attn = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, kk, vv), 5)
+    gb = n * k + 4 * n + 2 * k + 2 * n
+    ab = 2 * hkv * L * d * 2 + 2 * (2 * hq * d)
+    return {'gemv_1x2048_6144': {'us': round(t_gemv * 1e6, 1), 'achieved_gbps': round(gb / t_gemv / 1e9, 2)},
+            'attention_L32768': {'us': round(t_attn * 1e6, 1), 'achieved_gbps': round(ab / t_attn / 1e9, 2)},
+            'threads': threads}
+
+
 def copy_bandwidth(nbytes=1 << 30, reps=10):
     src = torch.empty(nbytes, dtype=torch.uint8, device='cuda')
     dst = torch.empty_like(src)
@@ -299,10 +374,13 @@ def main():
     if not args.no_extra:
         with torch.inference_mode():  # graph capture after the engine's inference-mode captures
             extra['attention'] = attention_roofline()
+            extra['attention_by_length'] = attention_sweep()
+            extra['gemv_1x2048_6144'] = gemv_cfg0()
             extra['copy_gbps'] = copy_bandwidth()
     cpu = None
     if args.cpu_tokens > 0 and gpu_tokens and args.model == 'qwen3-1.7b':
         cpu = cpu_baseline(eng, prompt, args.cpu_tokens, gpu_tokens)
+        cpu['kernels'] = cpu_kernels(cpu['cores'])
 
     wbytes, sbytes = cfg.weight_bytes()
     step_bytes = wbytes + sbytes + cfg.kv_bytes_per_slot() * mean_len + 2 * cfg.hidden

@@ -29,6 +29,7 @@ namespace {
 constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kChunk = kWave * 16;  // int8 elements covered by one 16-byte load per lane
+constexpr int kFusedMaxK = 12 * kChunk;  // the longest row egpt_int8_gemv_fused takes (include/egpt.h)
 
 enum { kEpiStore = 0, kEpiPartial = 1 };
 
@@ -264,6 +265,25 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
   const int st = check_gemv_args(x, ldx, w, ldw, scale, y, ldy, M, N, K);
   if (st != EGPT_OK) return st;
   if (M == 0 || N == 0) return EGPT_OK;
+  if (M == 1 && K >= 16 && K % 16 == 0 && K <= kFusedMaxK && ldw % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+      (uintptr_t)x % 16 == 0) {
+    // One aligned row: the fused kernel's plain store variant. It computes the
+    // same per-lane chunk sums in the same order and the same fixed row
+    // reduction, so the result is bit-identical, and it streams the weights in
+    // staged register buffers with exact wait counts.
+    egpt_gemv_fused d{};
+    d.epilogue = EGPT_EPI_STORE;
+    d.N = N;
+    d.K = K;
+    d.x = x;
+    d.x_ld = K;
+    d.x_rows = 1;
+    d.w = w;
+    d.ldw = ldw;
+    d.scale = scale;
+    d.y = y;
+    return egpt_int8_gemv_fused(&d, stream);
+  }
   GemvArgs a{(const uint16_t*)x, ldx, w, ldw, scale, y, ldy, M, N, K, K > 0 ? K : 1, 1};
   return launch_gemv<kEpiStore>(a, stream);
 }

@@ -159,3 +159,17 @@ def test_graph_capture_replay_bit_equal():
         eager = int8_linear(x * (i + 2), q, s)
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize('k,n', [(2048, 6144), (6144, 2048), (2048, 4096), (1024, 100), (12288, 4096), (2064, 48)])
+def test_single_row_matches_multi_row_kernel_bitwise(k, n):
+    """One aligned row goes to the fused kernel's store variant, two rows to gemv_i8_rows: both sum each lane's
+    1 KiB chunks in K order, remove 128 * sum(x) once and reduce the row in the same fixed order, so row 0 must
+    come out bit-identical either way."""
+    from efficientgpt_amd.int8_linear import int8_matmul
+    x, q, s = make_case(2, k, n, seed=k + n)
+    x, q, s = x.cuda(), q.cuda(), s.cuda()
+    one = int8_matmul(x[:1].contiguous(), q, s)
+    two = int8_matmul(torch.cat([x[:1], x[1:]]).contiguous(), q, s)
+    assert torch.equal(one[0], two[0])
+    check_against_oracle(one.cpu(), x[:1].cpu(), q.cpu(), s.cpu())
