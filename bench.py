@@ -192,7 +192,8 @@ def gemv_cfg0(n=6144, k=2048, sets=48, reps=10):
     return {'bound': 'hbm', 'achieved': round(nbytes / per_call / 1e9, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
             'frac': round(nbytes / per_call / 1e9 / HBM_PEAK_GBPS, 4), 'shape': f'1x{k} -> {n}',
             'bytes_per_call': nbytes, 'us_per_call': round(per_call * 1e6, 3),
-            'kernel': 'gemv_i8_rows (egpt_int8_gemv), cold, one call per weight copy'}
+            'kernel': 'egpt_int8_gemv (one aligned row: the fused kernel'"'"'s store variant), cold, one call per '
+                      'weight copy, each call including its hand-off from the previous launch'}
 
 
 def attention_sweep(lengths=(256, 1024, 4096, 16384)):

@@ -105,10 +105,50 @@ def _as_int8(weights, name):
     return quantize_weight(weights[name + '.weight'])
 
 
-class Qwen3Int8Engine:
-    """Static-cache batch-1 Qwen3 decoder with int8 linears; one graph replay per token."""
+def pack_qwen3(cfg, weights):
+    """The engine's packed int8 layout from transformers-named weights, on the device they are on.
 
-    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None):
+    Returns {'layers': [{'qkv_q', 'qkv_s', 'o_q', 'o_s', 'gu_q', 'gu_s', 'down_q', 'down_s', 'in_w', 'post_w',
+    'qn_w', 'kn_w'}, ...], 'embed', 'norm_w', 'head_q', 'head_s'}: linears given as `<name>.qweight` /
+    `<name>.scale` are taken as they are, float `<name>.weight` ones are quantised
+    (research/realmodel/int8_linear.py:106-117); a tied head is an int8 copy of the embedding
+    (int8_linear.py:154-155) and the embedding stays bf16.
+    """
+    bf = torch.bfloat16
+    layers = []
+    for i in range(cfg.layers):
+        p = f'model.layers.{i}.'
+        qs = [_as_int8(weights, p + n) for n in LINEARS]
+        layers.append({
+            'qkv_q': torch.cat([qs[0][0], qs[1][0], qs[2][0]]),
+            'qkv_s': torch.cat([qs[0][1], qs[1][1], qs[2][1]]).float(),
+            'o_q': qs[3][0], 'o_s': qs[3][1].float(),
+            'gu_q': torch.cat([qs[4][0], qs[5][0]]),
+            'gu_s': torch.cat([qs[4][1], qs[5][1]]).float(),
+            'down_q': qs[6][0], 'down_s': qs[6][1].float(),
+            'in_w': weights[p + 'input_layernorm.weight'].to(bf),
+            'post_w': weights[p + 'post_attention_layernorm.weight'].to(bf),
+            'qn_w': weights[p + 'self_attn.q_norm.weight'].to(bf),
+            'kn_w': weights[p + 'self_attn.k_norm.weight'].to(bf),
+        })
+        del qs
+    embed = weights['model.embed_tokens.weight'].to(bf)
+    if 'lm_head.qweight' in weights or 'lm_head.weight' in weights:
+        hq, hs = _as_int8(weights, 'lm_head')
+    else:
+        hq, hs = quantize_weight(embed)
+    return {'layers': layers, 'embed': embed, 'norm_w': weights['model.norm.weight'].to(bf),
+            'head_q': hq, 'head_s': hs.float()}
+
+
+class Qwen3Int8Engine:
+    """Static-cache batch-1 Qwen3 decoder with int8 linears; one graph replay per token.
+
+    `weights` holds transformers-named tensors (see pack_qwen3), or, with `packed=True`,
+    the packed layout pack_qwen3 returns (what efficientgpt_amd.checkpoint stores).
+    """
+
+    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False):
         if max_cache_len < 1:
             raise ValueError('max_cache_len must be >= 1')
         self.cfg, self.cap = cfg, int(max_cache_len)
@@ -121,31 +161,13 @@ class Qwen3Int8Engine:
         def put(t, dtype=None):
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
 
-        self.layers = []
-        for i in range(c.layers):
-            p = f'model.layers.{i}.'
-            qs = [_as_int8(weights, p + n) for n in LINEARS]
-            L = {
-                'qkv_q': put(torch.cat([qs[0][0], qs[1][0], qs[2][0]])),
-                'qkv_s': put(torch.cat([qs[0][1], qs[1][1], qs[2][1]]), torch.float32),
-                'o_q': put(qs[3][0]), 'o_s': put(qs[3][1], torch.float32),
-                'gu_q': put(torch.cat([qs[4][0], qs[5][0]])),
-                'gu_s': put(torch.cat([qs[4][1], qs[5][1]]), torch.float32),
-                'down_q': put(qs[6][0]), 'down_s': put(qs[6][1], torch.float32),
-                'in_w': put(weights[p + 'input_layernorm.weight'], bf),
-                'post_w': put(weights[p + 'post_attention_layernorm.weight'], bf),
-                'qn_w': put(weights[p + 'self_attn.q_norm.weight'], bf),
-                'kn_w': put(weights[p + 'self_attn.k_norm.weight'], bf),
-            }
-            self.layers.append(L)
-            del qs
-        self.embed = put(weights['model.embed_tokens.weight'], bf)
-        self.norm_w = put(weights['model.norm.weight'], bf)
-        if 'lm_head.qweight' in weights or 'lm_head.weight' in weights:
-            hq, hs = _as_int8(weights, 'lm_head')
-        else:  # tied: int8 copy of the embedding, the embedding stays bf16
-            hq, hs = quantize_weight(self.embed)
-        self.head_q, self.head_s = put(hq), put(hs, torch.float32)
+        pk = weights if packed else pack_qwen3(c, weights)
+        self.layers = [{k: put(v) for k, v in L.items()} for L in pk['layers']]
+        self.embed = put(pk['embed'], bf)
+        self.norm_w = put(pk['norm_w'], bf)
+        self.head_q, self.head_s = put(pk['head_q']), put(pk['head_s'], torch.float32)
+        self.inv_freq = None if inv_freq is None else inv_freq.detach().float().cpu()
+        del pk
         cos, sin = rope_tables(c, self.cap, inv_freq)
         self.cos, self.sin = put(cos), put(sin)
 
@@ -207,6 +229,13 @@ class Qwen3Int8Engine:
         self._step_c = d
 
     # ------------------------------------------------------------------ construction helpers
+
+    @classmethod
+    def from_int8(cls, path, max_cache_len, device='cuda'):
+        """Engine over an efficientgpt_amd.checkpoint file: the stored int8 layout, no re-quantisation."""
+        from .checkpoint import load_int8
+        cfg, packed, inv_freq = load_int8(path)
+        return cls(cfg, packed, max_cache_len, device=device, inv_freq=inv_freq, packed=True)
 
     @classmethod
     @torch.no_grad()

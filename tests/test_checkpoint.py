@@ -1,0 +1,55 @@
+"""The int8 on-disk format (efficientgpt_amd/checkpoint.py): a stored layout loads bit-identical, foreign or
+mismatched files are refused, and packing float weights quantises exactly as the reference's quantize_weight."""
+
+import os
+
+import pytest
+import torch
+
+from efficientgpt_amd import checkpoint
+from efficientgpt_amd.qwen3 import Qwen3Config, pack_qwen3
+from oracle.qwen3 import TINY, quantize_weights, random_weights
+
+CFG = Qwen3Config(TINY.vocab, TINY.hidden, TINY.inter, TINY.layers, TINY.heads, TINY.kv_heads, TINY.head_dim,
+                  TINY.rope_theta, TINY.rms_eps, TINY.tied)
+
+
+def packed_equal(a, b):
+    if len(a['layers']) != len(b['layers']):
+        return False
+    for la, lb in zip(a['layers'], b['layers']):
+        if la.keys() != lb.keys() or not all(la[k].dtype == lb[k].dtype and torch.equal(la[k], lb[k]) for k in la):
+            return False
+    return all(a[k].dtype == b[k].dtype and torch.equal(a[k], b[k]) for k in ('embed', 'norm_w', 'head_q', 'head_s'))
+
+
+def test_round_trip_is_bit_identical(tmp_path):
+    pk = pack_qwen3(CFG, quantize_weights(random_weights(TINY, seed=1, std=0.2), TINY))
+    inv = 1.0 / (1e4 ** (torch.arange(0, 32, 2).float() / 32))
+    path = os.path.join(tmp_path, 'tiny.safetensors')
+    checkpoint.save_int8(path, CFG, pk, inv_freq=inv)
+    cfg, got, inv2 = checkpoint.load_int8(path)
+    assert cfg == CFG
+    assert packed_equal(pk, got)
+    assert torch.equal(inv2, inv)
+
+
+def test_float_weights_pack_like_quantised_ones():
+    """Given float linears, pack_qwen3 quantises them (int8_linear.py:106-117); the result equals packing the
+    oracle's own quantisation of the same weights, tied head included."""
+    w = random_weights(TINY, seed=2, std=0.2)
+    assert packed_equal(pack_qwen3(CFG, w), pack_qwen3(CFG, quantize_weights(w, TINY)))
+
+
+def test_foreign_and_mismatched_files_are_refused(tmp_path):
+    from safetensors.torch import save_file
+    other = os.path.join(tmp_path, 'other.safetensors')
+    save_file({'x': torch.zeros(2)}, other, metadata={'format': 'pt'})
+    with pytest.raises(ValueError, match='not an'):
+        checkpoint.load_int8(other)
+    pk = pack_qwen3(CFG, quantize_weights(random_weights(TINY, seed=3, std=0.2), TINY))
+    pk['layers'][1]['o_q'] = pk['layers'][1]['o_q'][:, :-16].contiguous()
+    bad = os.path.join(tmp_path, 'bad.safetensors')
+    checkpoint.save_int8(bad, CFG, pk)
+    with pytest.raises(ValueError, match='layer 1 o_q'):
+        checkpoint.load_int8(bad)

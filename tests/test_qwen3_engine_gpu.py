@@ -249,3 +249,27 @@ def test_hf_attention_adapter_matches_oracle_attention():
         ref, margins, tops = oracle_greedy_with_margins(orc, x[0], 20)
         ok, where = near_tie_match(ref, got, margins, tops)
         assert ok, (p, where)
+
+
+def test_engine_from_int8_checkpoint_decodes_identically(tmp_path):
+    """save_engine -> Qwen3Int8Engine.from_int8: the same stored bytes, so the same logits and tokens, bit for bit."""
+    import os
+    from efficientgpt_amd import checkpoint
+    from efficientgpt_amd.qwen3 import Qwen3Int8Engine
+    eng, _ = build(SMALL, seed=4, std=0.15, cap=96)
+    path = os.path.join(tmp_path, 'small.safetensors')
+    checkpoint.save_engine(path, eng)
+    eng2 = Qwen3Int8Engine.from_int8(path, 96)
+    prompt = torch.randint(0, SMALL.vocab, (9,), generator=torch.Generator().manual_seed(5))
+    toks = []
+    for e in (eng, eng2):
+        e.reset()
+        logits = e.prefill(prompt).float().cpu()
+        e.capture()
+        seq = [int(e.token)]
+        for _ in range(12):
+            e.replay()
+            seq.append(int(e.token))
+        toks.append((logits, seq))
+    assert torch.equal(toks[0][0], toks[1][0])
+    assert toks[0][1] == toks[1][1]
