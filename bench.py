@@ -21,6 +21,7 @@ Prints one JSON line:
                   family (16 q / 8 kv heads, D 128, L = 32768), rotating > 512 MB of K/V
   attention_by_length  the same at L = 256 ... 16384
   gemv_1x2048_6144     the reference's headline GEMV shape through egpt_int8_gemv, cold
+  prefill_gemm         the MFMA prefill GEMM at the model's shapes, beside the reference's formula
   step            the whole step: weight + scale + KV bytes per token / ms per token
   copy_gbps       a device-to-device copy of 1 GiB, the measured bandwidth ceiling
   cpu_baseline    the CPU oracle (oracle/qwen3.py, torch on the host) on a bounded
@@ -194,6 +195,43 @@ def gemv_cfg0(n=6144, k=2048, sets=48, reps=10):
             'bytes_per_call': nbytes, 'us_per_call': round(per_call * 1e6, 3),
             'kernel': 'egpt_int8_gemv (one aligned row: the fused kernel'"'"'s store variant), cold, one call per '
                       'weight copy, each call including its hand-off from the previous launch'}
+
+
+def prefill_gemm(rows=(128, 1024), shapes=((4096, 2048), (12288, 2048), (2048, 6144)), reps=3):
+    """The prefill GEMM (egpt_int8_gemm, bf16 MFMA on int8 weights) at Qwen3-1.7B's QKV, gate/up and down
+    shapes, beside the reference's formula for the same product (research/realmodel/int8_linear.py:96-97:
+    dequantise to bf16, library GEMM, scale). TF/s of 2 M N K flops; peak dense bf16 MFMA 2500 TF/s."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device('cuda')
+    out = []
+    for m in rows:
+        for n, k in shapes:
+            g = torch.Generator(device=dev).manual_seed(0)
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            q = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+            sc = torch.rand(n, generator=g, device=dev) * 1e-3
+            y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+            calls = max(1, int(2e11 // (2 * m * n * k)))
+
+            def ours():
+                for _ in range(calls):
+                    _lib.check('egpt_int8_gemm', lib.egpt_int8_gemm(x.data_ptr(), k, q.data_ptr(), k, sc.data_ptr(),
+                                                                    y.data_ptr(), n, m, n, k, _lib.stream_ptr()))
+
+            def reference():
+                for _ in range(calls):
+                    ((x @ q.to(torch.bfloat16).t()).float() * sc).to(torch.bfloat16)
+
+            t_ours = _time_graph(ours, reps) / calls
+            t_ref = _time_graph(reference, reps) / calls
+            fl = 2 * m * n * k
+            out.append({'shape': f'{m}x{k} -> {n}', 'us': round(t_ours * 1e6, 1),
+                        'tflops': round(fl / t_ours / 1e12, 1), 'frac': round(fl / t_ours / 2.5e15, 4),
+                        'reference_formula_us': round(t_ref * 1e6, 1)})
+            del x, q, y
+    torch.cuda.empty_cache()
+    return out
 
 
 def attention_sweep(lengths=(256, 1024, 4096, 16384)):
@@ -377,6 +415,7 @@ def main():
             extra['attention'] = attention_roofline()
             extra['attention_by_length'] = attention_sweep()
             extra['gemv_1x2048_6144'] = gemv_cfg0()
+            extra['prefill_gemm'] = prefill_gemm()
             extra['copy_gbps'] = copy_bandwidth()
     cpu = None
     if args.cpu_tokens > 0 and gpu_tokens and args.model == 'qwen3-1.7b':

@@ -13,6 +13,7 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 LIB_PATH = Path(__file__).resolve().parent / 'libegpt_hip.so'
 
 EGPT_OK = 0
+EGPT_ERR_UNSUPPORTED = -2
 EGPT_F32, EGPT_BF16, EGPT_F16 = 0, 1, 2
 ABI_VERSION = 1
 
@@ -27,6 +28,7 @@ SIGNATURES = {
     'egpt_abi_version': (_c_int, []),
     'egpt_status_string': (ctypes.c_char_p, [_c_int]),
     'egpt_int8_gemv': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp]),
+    'egpt_int8_gemm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp]),
     'egpt_int8_gemv_splitk_workspace': (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
     'egpt_int8_gemv_splitk': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
                                        _c_int, _c_vp, _c_size, _c_vp]),

@@ -1,0 +1,271 @@
+// Int8-weight GEMM for prefill (more than 16 activation rows) on gfx950 MFMA.
+//
+//   y[m, n] = bf16( fp32( bf16( sum_k x[m, k] * w[n, k] ) ) * scale[n] )
+//
+// The reference's prefill formula (research/realmodel/int8_linear.py:96-97): a bf16
+// GEMM of x with the exact bf16 image of the int8 weights (fp32 accumulation,
+// rounded once to bf16), then the per-row scale in fp32 and a second bf16
+// rounding. The reference materialises w.to(bfloat16) and calls the library
+// GEMM; here the int8 rows go through LDS as int8 and each wavefront converts
+// its fragments to bf16 in registers, so the weights cross HBM once, as int8.
+//
+// Design:
+//   * A block of 4 wavefronts (2 x 2) computes a BM x BN tile of y; a wavefront
+//     owns (BM / 2) x (BN / 2) as 32 x 32 tiles of v_mfma_f32_32x32x16_bf16
+//     (fp32 accumulators, bf16 products exact).
+//   * K advances 64 at a time through two LDS buffers: the global loads of step
+//     k + 1 are issued before the MFMAs of step k and written to LDS after them;
+//     one barrier per step.
+//   * x rows sit in LDS as bf16 (64 + 8 padding, 144 bytes); weight rows stay int8
+//     (64 + 16 padding, 80 bytes) and a wavefront converts each 8-byte fragment
+//     to bf16 after reading it, so the weights cost half the LDS traffic. The
+//     padding puts the fragment reads of 16 consecutive rows on distinct banks.
+//   * int8 -> bf16 is exact: every value in [-127, 127] is a bf16.
+//   * Rows past M or N read a valid row and are never stored.
+// Operand layouts (checked on the MI355X): lane l holds A[l % 32][8 (l / 32) + e]
+// and B[8 (l / 32) + e][l % 32], e = 0..7; accumulator register r of lane l is
+// C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+#include "common.h"
+
+namespace egpt {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kBK = 64;               // K per LDS stage
+constexpr int kLdsRow = kBK + 8;      // bf16 elements per x row in LDS (16 bytes of padding)
+constexpr int kLdsRowW = kBK + 16;    // bytes per int8 weight row in LDS (16 bytes of padding)
+
+template <int BM, int BN>
+struct GemmShape {
+  static constexpr int TM = BM / 64;  // 32 x 32 tiles per wavefront along M
+  static constexpr int TN = BN / 64;  // ... along N
+  static constexpr int kALoads = BM * kBK * 2 / (kGemmThreads * 16);  // 16-byte x loads per thread per step
+  static constexpr int kBLoads = BN * kBK / (kGemmThreads * 16);      // 16-byte int8 loads per thread per step
+  static_assert(TM >= 1 && TN >= 1 && kALoads >= 1 && kBLoads >= 1, "tile too small for the block");
+};
+
+// 8 int8 (one LDS fragment) -> 8 bf16, exact.
+__device__ __forceinline__ bf16x8 int8x8_to_bf16(const uint32_t w0, const uint32_t w1) {
+  const uint32_t w[2] = {w0, w1};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float f0 = (float)(int)(int8_t)(w[i] & 0xffu);
+    const float f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
+    const float f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
+    const float f3 = (float)(int)(int8_t)(w[i] >> 24);
+    o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+    o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+  }
+  return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+struct GemmArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const int8_t* w;
+  int64_t ldw;
+  const float* scale;
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, K;
+  int tiles_m, tiles_n;
+};
+
+constexpr int kXcds = 8;        // MI355X: 8 XCDs, each with its own L2
+constexpr int kGroupM = 8;      // M tiles per group of the tile order
+
+// Block -> output tile. Blocks are dispatched round-robin to the XCDs (block b on
+// XCD b % 8), so XCD x is given the contiguous range of tile numbers
+// [start_x, start_x + count_x); within a range, tiles go in groups of kGroupM
+// M-tiles sweeping N. The blocks that run together on one XCD then share their x
+// and weight slices in that XCD's L2 instead of each streaming its own from HBM.
+// Both steps are bijections of [0, tiles), so every tile is computed once whatever
+// the dispatch order.
+__device__ __forceinline__ void gemm_tile(int b, int tiles_m, int tiles_n, int& pid_m, int& pid_n) {
+  const int tiles = tiles_m * tiles_n;
+  const int base = tiles / kXcds, extra = tiles % kXcds;
+  const int x = b % kXcds, j = b / kXcds;
+  const int t = x * base + min(x, extra) + j;
+  const int group = kGroupM * tiles_n;
+  const int first_m = (t / group) * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  pid_m = first_m + (t % group) % gm;
+  pid_n = (t % group) / gm;
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs a) {
+  using S = GemmShape<BM, BN>;
+  constexpr int TM = S::TM, TN = S::TN;
+  __shared__ __align__(16) uint16_t As[2][BM * kLdsRow];
+  __shared__ __align__(16) int8_t Bs[2][BN * kLdsRowW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int wm0 = (wave / 2) * (BM / 2);  // wavefront tile origin in the block tile
+  const int wn0 = (wave % 2) * (BN / 2);
+  int pid_m, pid_n;
+  gemm_tile(blockIdx.x, a.tiles_m, a.tiles_n, pid_m, pid_n);
+  const int64_t m0 = (int64_t)pid_m * BM;
+  const int64_t n0 = (int64_t)pid_n * BN;
+
+  // global -> register staging of one K step
+  const uint16_t* xsrc[S::kALoads];
+  int a_lds[S::kALoads];
+#pragma unroll
+  for (int j = 0; j < S::kALoads; ++j) {
+    const int i = tid + j * kGemmThreads;
+    const int row = i / (kBK / 8), chunk = i % (kBK / 8);
+    xsrc[j] = a.x + min(m0 + row, (int64_t)a.M - 1) * a.ldx + chunk * 8;
+    a_lds[j] = row * kLdsRow + chunk * 8;
+  }
+  const int8_t* wsrc[S::kBLoads];
+  int b_lds[S::kBLoads];
+#pragma unroll
+  for (int j = 0; j < S::kBLoads; ++j) {
+    const int i = tid + j * kGemmThreads;
+    const int row = i / (kBK / 16), chunk = i % (kBK / 16);
+    wsrc[j] = a.w + min(n0 + row, (int64_t)a.N - 1) * a.ldw + chunk * 16;
+    b_lds[j] = row * kLdsRowW + chunk * 16;
+  }
+  // Two register staging sets: the loads of step k + 2 are issued while step k is
+  // multiplied and land in LDS at the end of step k + 1, about two steps of MFMA
+  // work later. Loads past the last step re-read the last K slice (in bounds, never
+  // stored), so every load is unconditional and each wait is for one set only.
+  const int nk = a.K / kBK;
+  u32x4 xr[2][S::kALoads], wr[2][S::kBLoads];
+  auto load_step = [&](int kt, int set) {
+    const int k0 = min(kt, nk - 1) * kBK;
+#pragma unroll
+    for (int j = 0; j < S::kALoads; ++j) xr[set][j] = ld16(xsrc[j] + k0);
+#pragma unroll
+    for (int j = 0; j < S::kBLoads; ++j) wr[set][j] = ld16_stream(wsrc[j] + k0);
+  };
+  auto store_step = [&](int buf, int set) {
+#pragma unroll
+    for (int j = 0; j < S::kALoads; ++j) *(u32x4*)&As[buf][a_lds[j]] = xr[set][j];
+#pragma unroll
+    for (int j = 0; j < S::kBLoads; ++j) *(u32x4*)&Bs[buf][b_lds[j]] = wr[set][j];
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = f32x16{};
+
+  // fragment offsets (elements) inside one LDS buffer
+  const int frag_k = 8 * (lane / 32);
+  int a_frag[TM], b_frag[TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) a_frag[tm] = (wm0 + tm * 32 + lane % 32) * kLdsRow + frag_k;
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) b_frag[tn] = (wn0 + tn * 32 + lane % 32) * kLdsRowW + frag_k;
+
+  // The MFMAs of one K step from LDS buffer `buf`, 16 K columns at a time.
+  auto mma_step = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) af[tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
+        bfr[tn] = int8x8_to_bf16(p[0], p[1]);
+      }
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bfr[tn], acc[tm][tn], 0, 0, 0);
+    }
+  };
+
+  load_step(0, 0);
+  load_step(1, 1);
+  store_step(0, 0);
+  __syncthreads();
+  // Pairs of steps so the staging sets are fixed registers: step kt computes LDS
+  // buffer kt & 1, refills set kt & 1 with step kt + 2 and stores set (kt + 1) & 1;
+  // an odd last step runs after the loop. Scheduling barriers keep each phase in
+  // place (hoisting the second step's fragment reads above the first step's MFMAs
+  // would double the live registers).
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    load_step(kt + 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step(0);
+    __builtin_amdgcn_sched_barrier(0);
+    store_step(1, 1);
+    __syncthreads();
+    load_step(kt + 3, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step(1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 2 < nk) {
+      store_step(0, 0);
+      __syncthreads();
+    }
+  }
+  if (kt < nk) mma_step(0);
+
+  // y = bf16(bf16(acc) * scale): the reference's two roundings
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int64_t n = n0 + wn0 + tn * 32 + lane % 32;
+    const float sc = a.scale[min(n, (int64_t)a.N - 1)];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm0 + tm * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+        if (m < a.M && n < a.N) {
+          const float v = bf16_to_f32(f32_to_bf16(acc[tm][tn][r]));
+          a.y[m * a.ldy + n] = f32_to_bf16(v * sc);
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN>
+unsigned gemm_blocks(const GemmArgs& a) {
+  return (unsigned)(((int64_t)a.N + BN - 1) / BN) * (unsigned)(((int64_t)a.M + BM - 1) / BM);
+}
+
+template <int BM, int BN>
+int launch_gemm(GemmArgs a, hipStream_t st) {
+  a.tiles_m = (int)(((int64_t)a.M + BM - 1) / BM);
+  a.tiles_n = (int)(((int64_t)a.N + BN - 1) / BN);
+  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN>), dim3((unsigned)a.tiles_m * (unsigned)a.tiles_n),
+                     dim3(kGemmThreads), 0, st, a);
+  return EGPT_LAUNCH_STATUS();
+}
+
+}  // namespace
+}  // namespace egpt
+
+using namespace egpt;
+
+extern "C" int egpt_int8_gemm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y,
+                              int64_t ldy, int M, int N, int K, hipStream_t stream) {
+  if (!x || !w || !scale || !y || M < 0 || N < 0 || K < 0) return EGPT_ERR_INVALID;
+  if (ldx < K || ldw < K || ldy < N) return EGPT_ERR_INVALID;
+  if (M == 0 || N == 0) return EGPT_OK;
+  if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
+    return EGPT_ERR_UNSUPPORTED;
+  if (((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX) return EGPT_ERR_UNSUPPORTED;
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0};
+  // The largest tile that still gives every CU a block; small M keeps more, narrower tiles.
+  if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm<256, 256>(a, stream);
+  if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256>(a, stream);
+  if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128>(a, stream);
+  if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
+  return launch_gemm<64, 64>(a, stream);
+}

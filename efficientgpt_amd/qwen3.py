@@ -33,7 +33,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .int8_linear import MAX_DECODE_ROWS, quantize_weight
+from .int8_linear import MAX_DECODE_ROWS, int8_gemm, quantize_weight
 
 # Prompts longer than this take the library-GEMM attention in prefill.
 PREFILL_KERNEL_MAX_ROWS = 64
@@ -290,13 +290,14 @@ class Qwen3Int8Engine:
         return _lib.stream_ptr(self.device)
 
     def _linear(self, x, q, s, out, rows):
-        """out[:rows] = int8 linear of x[:rows]; the reference's row rule (<= 16 rows: GEMV kernel)."""
+        """out[:rows] = int8 linear of x[:rows]; the reference's row rule (<= 16 rows: GEMV kernel, more: the
+        prefill GEMM)."""
         if rows <= MAX_DECODE_ROWS:
             _lib.check('egpt_int8_gemv', _lib.lib().egpt_int8_gemv(
                 x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), s.data_ptr(), out.data_ptr(), out.stride(0),
                 rows, q.shape[0], q.shape[1], self._stream()))
         else:
-            out[:rows] = ((x[:rows] @ q.to(torch.bfloat16).t()).float() * s).to(torch.bfloat16)
+            int8_gemm(x[:rows], q, s, out=out[:rows])
 
     def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first, pos0=0):
         lib, c, L, st = _lib.lib(), self.cfg, self.layers[i], self._stream()

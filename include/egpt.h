@@ -65,6 +65,20 @@ int egpt_int8_gemv_splitk(const void *x, int64_t ldx, const int8_t *w, int64_t l
                           void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Int8-weight GEMM for prefill (any M, typically > 16 rows):
+ *   y[m, n] = bf16( fp32( bf16( sum_k x[m, k] * w[n, k] ) ) * scale[n] )
+ * fp32 accumulation on bf16 MFMA with the weights' exact bf16 image, rounded once to
+ * bf16, then the scale in fp32 and a second rounding: the reference's prefill formula
+ * `((x2 @ w.to(bfloat16).t()).float() * s).to(bfloat16)` (research/realmodel/int8_linear.py:96-97),
+ * without materialising the bf16 weights. x bf16 [M, K] (row stride ldx), w int8 [N, K]
+ * (ldw), y bf16 [M, N] (ldy). Needs K a multiple of 64, ldx % 8 == 0, ldw % 16 == 0 and
+ * 16-byte aligned x and w; returns EGPT_ERR_UNSUPPORTED otherwise (the caller keeps the
+ * library formula for such shapes).
+ */
+int egpt_int8_gemm(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                   void *y, int64_t ldy, int M, int N, int K, hipStream_t stream);
+
+/*
  * Split-K GQA decode attention (flash decoding) with its partial-softmax reduce.
  *   q   [B, Hq, 1, D]     strides (q_sb, q_sh), last dim contiguous
  *   k,v [B, Hkv, cap, D]  strides (sb, sh, sn), last dim contiguous

@@ -39,12 +39,15 @@ def bf16_ulp(y):
 def check_against_oracle(y, x, q, s, min_exact=0.99):
     """Reference tolerance vs fp64 truth, and within one bf16 ulp of the oracle's formula for the row count.
 
-    Past 16 rows the op takes the library GEMM (two bf16 roundings, the reference's
-    prefill formula), whose accumulation order may move the intermediate by one ulp:
-    there two ulps and 90 % bit-exact are allowed.
+    Past 16 rows the op takes the prefill GEMM (the reference's formula, two bf16
+    roundings). Its fp32 sums over K run in the MFMA order; the oracle sums exactly. An
+    fp32 sum of K terms is off by about sqrt(K) 2^-24 sum|x q| (a random-walk bound),
+    which near a cancelling zero is many ulps of a tiny output. So there each element
+    may differ by three ulps (one per rounding, plus one) plus that sum error times the
+    scale, and 90 % must be bit-exact. torch's own bf16 GEMM of the same formula needs
+    the allowance too (up to 99 ulps at outputs near 1e-6 on these shapes).
     """
     prefill = x.shape[0] > oint8.MAX_DECODE_ROWS
-    ulps = 2.0 if prefill else 1.0
     min_exact = 0.9 if prefill else min_exact
     yn = y.float().cpu().numpy()
     xn, qn, sn = x.float().numpy(), q.numpy(), s.numpy()
@@ -52,7 +55,12 @@ def check_against_oracle(y, x, q, s, min_exact=0.99):
     assert err <= oint8.tolerance_vs_naive(xn, qn, sn), err
     want = oint8.linear(xn, qn, sn)
     diff = np.abs(yn.astype(np.float64) - want)
-    assert np.all(diff <= ulps * bf16_ulp(want)), float(diff.max())
+    if prefill:
+        sum_abs = (np.abs(xn).astype(np.float64) @ np.abs(qn).astype(np.float64).T) * sn[None, :]
+        bound = 3.0 * bf16_ulp(want) + 2.0 ** -24 * np.sqrt(xn.shape[1]) * sum_abs
+    else:
+        bound = bf16_ulp(want)
+    assert np.all(diff <= bound), float((diff - bound).max())
     assert np.mean(diff == 0) >= min_exact, float(np.mean(diff == 0))
     rel = np.abs(yn - oint8.linear_truth(xn, qn, sn)).max() / max(np.abs(oint8.linear_truth(xn, qn, sn)).max(), 1e-30)
     assert rel <= 2e-2
@@ -173,3 +181,41 @@ def test_single_row_matches_multi_row_kernel_bitwise(k, n):
     two = int8_matmul(torch.cat([x[:1], x[1:]]).contiguous(), q, s)
     assert torch.equal(one[0], two[0])
     check_against_oracle(one.cpu(), x[:1].cpu(), q.cpu(), s.cpu())
+
+
+PREFILL_SHAPES = [(17, 64, 64), (33, 2048, 4096), (128, 2048, 4096), (100, 2048, 6144), (300, 6144, 2048),
+                  (1000, 1024, 96), (257, 4096, 1000), (4096, 2048, 2048), (300, 192, 4096), (4096, 128, 4096)]
+
+
+@pytest.mark.parametrize('m,k,n', PREFILL_SHAPES)
+def test_prefill_gemm_kernel_matches_oracle(m, k, n):
+    """More than 16 rows: the MFMA GEMM (egpt_int8_gemm), against the oracle's prefill formula
+    bf16(fp32(bf16(x q^T)) s) and the reference's tolerance; odd N and M exercise the masked edges,
+    K = 192 an odd number of 64-wide K steps, and the last two shapes the 128 x 256 and 256 x 256 tiles."""
+    from efficientgpt_amd import _lib
+    x, q, s = make_case(m, k, n, seed=m + k + n)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    y = torch.empty(m, n, device='cuda', dtype=torch.bfloat16)
+    st = _lib.lib().egpt_int8_gemm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), y.data_ptr(), n, m, n, k,
+                                   _lib.stream_ptr())
+    assert st == 0, st  # aligned shapes take the kernel, not the library formula
+    check_against_oracle(y.cpu(), x, q, s)
+    lib_form = ((xd @ qd.to(torch.bfloat16).t()).float() * sd).to(torch.bfloat16)
+    diff = (y.float() - lib_form.float()).abs()
+    assert float((diff == 0).float().mean()) >= 0.9
+
+
+def test_prefill_op_uses_kernel_and_falls_back_for_unaligned_k():
+    from efficientgpt_amd import _lib
+    from efficientgpt_amd.int8_linear import int8_linear
+    x, q, s = make_case(40, 100, 70, seed=9)  # K = 100: not a multiple of 64
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    st = _lib.lib().egpt_int8_gemm(xd.data_ptr(), 100, qd.data_ptr(), 100, sd.data_ptr(),
+                                   torch.empty(40, 70, device='cuda', dtype=torch.bfloat16).data_ptr(), 70, 40, 70,
+                                   100, _lib.stream_ptr())
+    assert st == _lib.EGPT_ERR_UNSUPPORTED
+    check_against_oracle(int8_linear(xd, qd, sd).cpu(), x, q, s)
+    x, q, s = make_case(48, 2048, 512, seed=11)
+    y = int8_linear(x.cuda().view(4, 12, 2048), q.cuda(), s.cuda())  # leading dims, kernel path
+    assert y.shape == (4, 12, 512)
+    check_against_oracle(y.view(48, 512).cpu(), x, q, s)
