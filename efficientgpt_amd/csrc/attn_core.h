@@ -198,15 +198,19 @@ __device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float
 // of every query head to
 //   ws_m[row + g * nsplit], ws_l[...], ws_acc[(row + g * nsplit) * D + d]
 // where row = (b * Hq + hk * G) * nsplit + split. An empty range with no extra
-// slot gives the empty state (m = -inf, l = 0, acc = 0). Must be called by all
-// NT threads of the block.
+// slot gives the empty state (m = -inf, l = 0, acc = 0). With `out` set (one
+// split covering every live slot) the block writes the attention output itself,
+// out[g * o_sh + d] = acc / l, instead of the partials: the value the combine
+// would compute, whose single weight exp(m - m) is 1. Must be called by all NT
+// threads of the block.
 template <typename Geo, typename T, int G, int LPR, int U>
 __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], AttnPipe<LPR, U>& pp,
                                              const T* __restrict__ kbase, int64_t k_sn, const T* __restrict__ vbase,
                                              int64_t v_sn, int64_t start, int64_t end, float scale,
                                              float* __restrict__ ws_m, float* __restrict__ ws_l,
                                              float* __restrict__ ws_acc, int64_t row, int nsplit,
-                                             const float* xk = nullptr, const float* xv = nullptr) {
+                                             const float* xk = nullptr, const float* xv = nullptr,
+                                             T* __restrict__ out = nullptr, int64_t o_sh = 0) {
   constexpr int EPL = Geo::EPL;
   constexpr int EPV = Geo::EPV;
   constexpr int LPS = Geo::LPS;
@@ -349,6 +353,10 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
         a = fmaf(wj, sm_acc[j][g][d], a);
         ls = fmaf(wj, sm_l[j][g], ls);
       }
+    }
+    if (out) {
+      Elem<T>::store1(out + (int64_t)g * o_sh + d, a / ls);
+      continue;
     }
     const int64_t slot = row + (int64_t)g * nsplit;
     ws_acc[slot * D + d] = a;

@@ -25,7 +25,8 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(
     const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ k, int64_t k_sb, int64_t k_sh,
     int64_t k_sn, const T* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
     const int64_t* __restrict__ position, int64_t pos_stride, float* __restrict__ ws_m, float* __restrict__ ws_l,
-    float* __restrict__ ws_acc, int Hkv, int cap, int nsplit, float scale) {
+    float* __restrict__ ws_acc, int Hkv, int cap, int nsplit, float scale, T* __restrict__ out, int64_t o_sb,
+    int64_t o_sh) {
   constexpr int LPR = kSplitLPR<T>;
   constexpr int U = G >= 8 ? 2 : kSplitUnroll<T>;  // G >= 8: two buffers of 4 slots spill
   using Geo = AttnGeom<T, D, NT, LPR, U>;
@@ -57,8 +58,10 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < LPR; ++j) Elem<T>::unpack(qr[g][j], &qf[g][j * EPV]);
+  // One split: the block writes the output rows of its G query heads (no combine launch).
+  T* o = nsplit == 1 ? out + (int64_t)b * o_sb + (int64_t)(hk * G) * o_sh : nullptr;
   attn_partial<Geo, T, G>(qf, pp, kb, k_sn, vb, v_sn, start, end, scale, ws_m, ws_l, ws_acc,
-                          ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit);
+                          ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit, nullptr, nullptr, o, o_sh);
 }
 
 // Partial-softmax reduce: one block of kCombineThreads per (b, query head).
@@ -96,8 +99,10 @@ int launch_attn(const AttnArgs& a, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.Hkv), (unsigned)a.nsplit);
   hipLaunchKernelGGL((attn_split_kernel<T, D, G>), grid, dim3(kAttnThreads), 0, st, (const T*)a.q, a.q_sb, a.q_sh,
                      (const T*)a.k, a.k_sb, a.k_sh, a.k_sn, (const T*)a.v, a.v_sb, a.v_sh, a.v_sn, a.position,
-                     a.pos_stride, a.ws_m, a.ws_l, a.ws_acc, a.Hkv, a.cap, a.nsplit, a.scale);
+                     a.pos_stride, a.ws_m, a.ws_l, a.ws_acc, a.Hkv, a.cap, a.nsplit, a.scale, (T*)a.out, a.o_sb,
+                     a.o_sh);
   if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
+  if (a.nsplit == 1) return EGPT_OK;  // the split kernel wrote the output
   hipLaunchKernelGGL((attn_combine_kernel<T, D>), dim3((unsigned)(a.B * a.Hq)), dim3(kCombineThreads), 0, st,
                      a.ws_m, a.ws_l, a.ws_acc, (T*)a.out, a.o_sb, a.o_sh, a.Hq, a.nsplit);
   return EGPT_LAUNCH_STATUS();

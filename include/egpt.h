@@ -92,7 +92,7 @@ int egpt_int8_gemm(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, con
  * With Hkv == Hq this is the reference's MHA contract.
  * Replaces _split_kernel + _combine_kernel and the NSPLIT choice
  * (research/phase5/decode_attention.py:22-71, :74-103); nsplit 1 is the
- * single-pass kernel (:106-151).
+ * single-pass kernel (:106-151): one launch, which writes out directly.
  */
 int egpt_decode_attn_default_splits(int B, int Hkv, int cap);
 int egpt_decode_attn_workspace(int B, int Hq, int Hkv, int cap, int D, int nsplit, size_t *bytes);
