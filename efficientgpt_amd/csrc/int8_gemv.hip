@@ -157,6 +157,105 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_i8_generic(
   }
 }
 
+// Small batches (3 <= M <= 16 activation rows) on MFMA. At M rows a weight byte
+// feeds M products; on the vector ALU that is M FMAs per byte and 8 rows already
+// run at a fifth of the single-row bandwidth. v_mfma_f32_16x16x32_bf16 takes the
+// activation rows as A (rows past M are clamped copies, never stored) and 16
+// weight rows, converted exactly to bf16, as B. A dot product does not care
+// about K order, so lane l owns 16 contiguous K of weight row n0 + l % 16 and of
+// activation row l % 16 (K group l / 16); its two 8-element halves feed the two
+// MFMAs of a 64-wide step. G wavefronts share 16 output features: wavefront j
+// of the group takes the steps j, j + G, ... and the G partial tiles are summed
+// through LDS in wavefront order (a fixed order: bitwise reproducible). Then
+// y = bf16(scale * sum), the decode rounding.
+// Layouts (checked on the MI355X): lane l holds A[l % 16][8 (l / 16) + e] and
+// B[8 (l / 16) + e][l % 16]; accumulator register r is C[4 (l / 16) + r][l % 16].
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaStage = 4;  // 64-wide K steps whose loads are issued together
+
+__device__ __forceinline__ bf16x8_t int8x8_bf16(uint32_t w0, uint32_t w1) {
+  const uint32_t w[2] = {w0, w1};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float f0 = (float)(int)(int8_t)(w[i] & 0xffu);
+    const float f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
+    const float f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
+    const float f3 = (float)(int)(int8_t)(w[i] >> 24);
+    o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+    o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+  }
+  return __builtin_bit_cast(bf16x8_t, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// G wavefronts share a group of 16 features (8 / G groups per block); with G = 1
+// each wavefront would stream its 16 rows over all of K and store its own outputs.
+template <int G>
+__global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, uint16_t* __restrict__ y, int64_t ldy, int m_rows, int N, int K) {
+  __shared__ float red[G > 1 ? kMfmaWaves : 1][256];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int group = wave / G, sub = wave % G;
+  const int64_t n0 = ((int64_t)blockIdx.x * (kMfmaWaves / G) + group) * 16;
+  const int8_t* wrow = w + min(n0 + lane % 16, (int64_t)N - 1) * ldw + 16 * (lane / 16);
+  const uint16_t* xrow = x + (int64_t)min(lane % 16, m_rows - 1) * ldx + 16 * (lane / 16);
+  const int steps = K / 64;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = sub; s0 < steps; s0 += G * kMfmaStage) {
+    u32x4 wv[kMfmaStage], xa[kMfmaStage], xb[kMfmaStage];
+#pragma unroll
+    for (int j = 0; j < kMfmaStage; ++j) {
+      const int st = min(s0 + j * G, steps - 1);  // past the end: a valid step, not accumulated
+      wv[j] = ld16_stream(wrow + st * 64);
+      xa[j] = ld16(xrow + st * 64);
+      xb[j] = ld16(xrow + st * 64 + 8);
+    }
+#pragma unroll
+    for (int j = 0; j < kMfmaStage; ++j) {
+      if (s0 + j * G < steps) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[j]),
+                                                      int8x8_bf16(wv[j].x, wv[j].y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xb[j]),
+                                                      int8x8_bf16(wv[j].z, wv[j].w), acc, 0, 0, 0);
+      }
+    }
+  }
+  if constexpr (G > 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][(4 * (lane / 16) + r) * 16 + lane % 16] = acc[r];
+    __syncthreads();
+    // each group's G partials summed in wavefront order, one output per thread
+    for (int e = threadIdx.x; e < (kMfmaWaves / G) * 256; e += kMfmaWaves * kWave) {
+      const int gi = e / 256, idx = e % 256;
+      float sum = red[gi * G][idx];
+#pragma unroll
+      for (int j = 1; j < G; ++j) sum += red[gi * G + j][idx];
+      const int m = idx / 16;
+      const int64_t nn = ((int64_t)blockIdx.x * (kMfmaWaves / G) + gi) * 16 + idx % 16;
+      if (m < m_rows && nn < N) y[(int64_t)m * ldy + nn] = f32_to_bf16(sum * scale[nn]);
+    }
+  } else {
+    const int64_t n = n0 + lane % 16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * (lane / 16) + r;
+      if (m < m_rows && n < N) y[(int64_t)m * ldy + n] = f32_to_bf16(acc[r] * scale[n]);
+    }
+  }
+}
+
+template <int G>
+void launch_mfma(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
+                 int64_t ldy, int M, int N, int K, hipStream_t st) {
+  const int64_t per_block = 16 * (kMfmaWaves / G);
+  hipLaunchKernelGGL((gemv_i8_mfma<G>), dim3((unsigned)((N + per_block - 1) / per_block)), dim3(kMfmaWaves * kWave),
+                     0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K);
+}
+
 // Deterministic split-K reduction: fixed split order, then scale, one rounding.
 __global__ __launch_bounds__(256) void gemv_splitk_reduce(const float* __restrict__ part, int splits, int m_rows,
                                                           int N, const float* __restrict__ scale,
@@ -283,6 +382,17 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
     d.scale = scale;
     d.y = y;
     return egpt_int8_gemv_fused(&d, stream);
+  }
+  if (M >= 3 && K >= 64 && K % 64 == 0 && ldw % 16 == 0 && ldx % 8 == 0 && (uintptr_t)w % 16 == 0 &&
+      (uintptr_t)x % 16 == 0) {
+    // 3-16 rows: MFMA (two rows stay on the vector kernel, which is faster there)
+    const uint16_t* xx = (const uint16_t*)x;
+    uint16_t* yy = (uint16_t*)y;
+    // all 8 wavefronts on one 16-feature group: splitting K eight ways keeps the most
+    // loads in flight (measured faster than 1, 2 or 4 wavefronts per group at every
+    // Qwen3-1.7B shape, the 151936-row lm_head included)
+    launch_mfma<kMfmaWaves>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+    return EGPT_LAUNCH_STATUS();
   }
   GemvArgs a{(const uint16_t*)x, ldx, w, ldw, scale, y, ldy, M, N, K, K > 0 ? K : 1, 1};
   return launch_gemv<kEpiStore>(a, stream);

@@ -40,12 +40,14 @@ def check_against_oracle(y, x, q, s, min_exact=0.99):
     """Reference tolerance vs fp64 truth, and within one bf16 ulp of the oracle's formula for the row count.
 
     Past 16 rows the op takes the prefill GEMM (the reference's formula, two bf16
-    roundings). Its fp32 sums over K run in the MFMA order; the oracle sums exactly. An
+    roundings), and 3-16 rows the small-batch MFMA kernel (one rounding). Their fp32
+    sums over K run in the MFMA order; the oracle sums exactly. An
     fp32 sum of K terms is off by about sqrt(K) 2^-24 sum|x q| (a random-walk bound),
     which near a cancelling zero is many ulps of a tiny output. So there each element
-    may differ by three ulps (one per rounding, plus one) plus that sum error times the
-    scale, and 90 % must be bit-exact. torch's own bf16 GEMM of the same formula needs
-    the allowance too (up to 99 ulps at outputs near 1e-6 on these shapes).
+    may differ by that sum error times the scale plus one ulp per rounding (three for
+    the two-rounding prefill form); 90 % (prefill) or 99 % must be bit-exact. torch's own
+    bf16 GEMM of the same formula needs the allowance too (up to 99 ulps at outputs near
+    1e-6 on these shapes).
     """
     prefill = x.shape[0] > oint8.MAX_DECODE_ROWS
     min_exact = 0.9 if prefill else min_exact
@@ -55,9 +57,12 @@ def check_against_oracle(y, x, q, s, min_exact=0.99):
     assert err <= oint8.tolerance_vs_naive(xn, qn, sn), err
     want = oint8.linear(xn, qn, sn)
     diff = np.abs(yn.astype(np.float64) - want)
+    sum_abs = (np.abs(xn).astype(np.float64) @ np.abs(qn).astype(np.float64).T) * sn[None, :]
+    sum_err = 2.0 ** -24 * np.sqrt(xn.shape[1]) * sum_abs
     if prefill:
-        sum_abs = (np.abs(xn).astype(np.float64) @ np.abs(qn).astype(np.float64).T) * sn[None, :]
-        bound = 3.0 * bf16_ulp(want) + 2.0 ** -24 * np.sqrt(xn.shape[1]) * sum_abs
+        bound = 3.0 * bf16_ulp(want) + sum_err
+    elif xn.shape[0] > 2:  # 3-16 rows: the MFMA kernel, fp32 sums in the MFMA's order
+        bound = bf16_ulp(want) + sum_err
     else:
         bound = bf16_ulp(want)
     assert np.all(diff <= bound), float((diff - bound).max())
@@ -170,17 +175,36 @@ def test_graph_capture_replay_bit_equal():
 
 
 @pytest.mark.parametrize('k,n', [(2048, 6144), (6144, 2048), (2048, 4096), (1024, 100), (12288, 4096), (2064, 48)])
-def test_single_row_matches_multi_row_kernel_bitwise(k, n):
-    """One aligned row goes to the fused kernel's store variant, two rows to gemv_i8_rows: both sum each lane's
-    1 KiB chunks in K order, remove 128 * sum(x) once and reduce the row in the same fixed order, so row 0 must
-    come out bit-identical either way."""
+def test_single_row_matches_row_kernel_bitwise(k, n):
+    """One aligned row goes to the fused kernel's store variant; the split-K entry with one split runs
+    gemv_i8_rows and adds its single partial to zero. Both sum each lane's 1 KiB chunks in K order, remove
+    128 * sum(x) once and reduce the row in the same fixed order, so the outputs must be bit-identical."""
+    from efficientgpt_amd import _lib
     from efficientgpt_amd.int8_linear import int8_matmul
-    x, q, s = make_case(2, k, n, seed=k + n)
+    x, q, s = make_case(1, k, n, seed=k + n)
     x, q, s = x.cuda(), q.cuda(), s.cuda()
-    one = int8_matmul(x[:1].contiguous(), q, s)
-    two = int8_matmul(torch.cat([x[:1], x[1:]]).contiguous(), q, s)
-    assert torch.equal(one[0], two[0])
-    check_against_oracle(one.cpu(), x[:1].cpu(), q.cpu(), s.cpu())
+    one = int8_matmul(x, q, s)
+    ref = torch.empty_like(one)
+    ws = torch.empty(max(4 * n, 4), device='cuda', dtype=torch.uint8)
+    _lib.check('egpt_int8_gemv_splitk', _lib.lib().egpt_int8_gemv_splitk(
+        x.data_ptr(), k, q.data_ptr(), k, s.data_ptr(), ref.data_ptr(), n, 1, n, k, 1, ws.data_ptr(), ws.numel(),
+        _lib.stream_ptr()))
+    assert torch.equal(one, ref)
+    check_against_oracle(one.cpu(), x.cpu(), q.cpu(), s.cpu())
+
+
+@pytest.mark.parametrize('m', [3, 4, 8, 16])
+@pytest.mark.parametrize('k,n', [(2048, 4096), (6144, 2048), (2048, 100), (12288, 48), (512, 32768)])
+def test_small_batch_mfma_kernel_matches_oracle(m, k, n):
+    """3-16 rows take the MFMA kernel (K a multiple of 64, aligned rows): against the oracle's decode
+    rule, odd N, the longest K, and 2048 feature groups (32768 features)."""
+    from efficientgpt_amd.int8_linear import int8_matmul
+    x, q, s = make_case(m, k, n, seed=100 + m + k + n)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    y = int8_matmul(xd, qd, sd)
+    check_against_oracle(y.cpu(), x, q, s)
+    again = int8_matmul(xd, qd, sd)
+    assert torch.equal(y, again)  # fixed reduction order: reproducible
 
 
 PREFILL_SHAPES = [(17, 64, 64), (33, 2048, 4096), (128, 2048, 4096), (100, 2048, 6144), (300, 6144, 2048),
