@@ -65,12 +65,29 @@ template <> struct Elem<_Float16> {
 
 // ---------------------------------------------------------------- loads
 
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+// Global-memory accessors. Every pointer the kernels dereference through them is
+// device (global) memory; the address-space cast makes the compiler emit global_*
+// instructions even for pointers it cannot trace to a kernel argument (read from
+// a table in memory, say). A generic pointer would give flat_* instructions, which
+// also count against lgkmcnt, so every LDS wait would then wait for them too.
+template <typename T>
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+  return *(global_ptr<const T>)p;
+}
+template <typename T>
+__device__ __forceinline__ void gstore(T* p, T v) {
+  *(global_ptr<T>)p = v;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(global_ptr<const u32x4>)p; }
 
 // Streaming load for data read exactly once (weights): non-temporal hint keeps it
 // from evicting the small, re-read operands (activations, scales) from L2.
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
-  return __builtin_nontemporal_load((const u32x4*)p);
+  return __builtin_nontemporal_load((global_ptr<const u32x4>)p);
 }
 
 // ---------------------------------------------------------------- DPP reductions

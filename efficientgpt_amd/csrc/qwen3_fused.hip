@@ -27,7 +27,7 @@
 // by the kernel boundary. (A last-block-done hand-off inside the lm_head launch
 // needs a device-scope fence per block; 9.5k blocks of L2 write-back/invalidate
 // made that launch 30x slower than the stream itself.)
-#include "attn_core.h"
+#include "step_core.h"
 
 namespace egpt {
 namespace {
@@ -38,8 +38,6 @@ constexpr int kFChunk = kWave * 16;  // int8 weights covered by one 16-byte load
 constexpr int kMaxChunks = 12;       // K <= 12288
 
 enum { kEpiStore = 0, kEpiResid = 1, kEpiSwiGLU = 2, kEpiArgmax = 3 };
-
-__device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 struct FusedGemv {
   const uint16_t* x;       // activation row, or a table when x_token is set
@@ -65,71 +63,6 @@ struct FusedGemv {
   int nsplit;
   int head_dim;
 };
-
-// 16 int8 weights times 16 fp32 activations, biased form: (w + 128) converts
-// with one v_cvt_f32_ubyteN; 128 * sum(x) is removed once after the reduction.
-__device__ __forceinline__ float dot16_biased(const u32x4 wq, const float* xf, float acc) {
-  const uint32_t d[4] = {wq.x ^ 0x80808080u, wq.y ^ 0x80808080u, wq.z ^ 0x80808080u, wq.w ^ 0x80808080u};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    acc = fmaf((float)(d[j] & 0xffu), xf[4 * j + 0], acc);
-    acc = fmaf((float)((d[j] >> 8) & 0xffu), xf[4 * j + 1], acc);
-    acc = fmaf((float)((d[j] >> 16) & 0xffu), xf[4 * j + 2], acc);
-    acc = fmaf((float)(d[j] >> 24), xf[4 * j + 3], acc);
-  }
-  return acc;
-}
-
-__device__ __forceinline__ void unpack_bf16x16(const u32x4 a, const u32x4 b, float* xf) {
-  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    xf[2 * i] = bf16_lo(u[i]);
-    xf[2 * i + 1] = bf16_hi(u[i]);
-  }
-}
-
-struct ArgBest {
-  float v;
-  int i;
-};
-
-// larger value wins; equal values: the smaller index (torch.argmax's first maximum)
-__device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
-  return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
-}
-
-template <int W>
-__device__ __forceinline__ ArgBest block_argbest(ArgBest x) {
-  __shared__ float sv[W];
-  __shared__ int si[W];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    ArgBest o;
-    o.v = __shfl_xor(x.v, off, kWave);
-    o.i = __shfl_xor(x.i, off, kWave);
-    x = arg_better(x, o);
-  }
-  const int wave = threadIdx.x / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    sv[wave] = x.v;
-    si[wave] = x.i;
-  }
-  lds_barrier();
-  ArgBest r{sv[0], si[0]};
-#pragma unroll
-  for (int j = 1; j < W; ++j) r = arg_better(r, ArgBest{sv[j], si[j]});
-  lds_barrier();
-  return r;
-}
-
-__device__ __forceinline__ const uint16_t* token_row(const uint16_t* base, const int64_t* token, int64_t ld,
-                                                     int rows) {
-  if (!token) return base;
-  int64_t t = *token;
-  t = t < 0 ? 0 : (t >= rows ? rows - 1 : t);
-  return base + t * ld;
-}
 
 // Activation source of a fused GEMV.
 enum { kXRow = 0, kXMerge = 1 };
@@ -533,34 +466,6 @@ struct AttnStep {
   float eps, scale;
 };
 
-// Head-wise RMSNorm + RoPE of one head held by an LPS-lane group (EPL elements
-// per lane, element d0 + e; x, norm weight, cos and sin rows already loaded).
-// rotate_half pairs element i with i +- D/2, which sits in lane (sub ^ LPS/2)
-// at the same e.
-template <int D, int EPL, int LPS>
-__device__ __forceinline__ void head_norm_rope(const u32x4 xr, const u32x4 wr, const u32x4 cr, const u32x4 sr, int d0,
-                                               float eps, float (&out)[EPL]) {
-  float xv[EPL], w[EPL], cs[EPL], sn[EPL];
-  Elem<__bf16>::unpack(xr, xv);
-  Elem<__bf16>::unpack(wr, w);
-  Elem<__bf16>::unpack(cr, cs);
-  Elem<__bf16>::unpack(sr, sn);
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) ss = fmaf(xv[e], xv[e], ss);
-  const float inv = rsqrtf(group_sum<LPS>(ss) / (float)D + eps);
-  float nv[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) nv[e] = bf16r(w[e] * bf16r(xv[e] * inv));
-  const bool lower = d0 < D / 2;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const float p = __shfl_xor(nv[e], LPS / 2, kWave);
-    const float rh = lower ? -p : p;
-    out[e] = bf16r(bf16r(nv[e] * cs[e]) + bf16r(rh * sn[e]));
-  }
-}
-
 // Attention partials of one decode step: block (kv head, split). Every load
 // that does not depend on arithmetic is issued first (queries, new key and
 // value, norm weights, RoPE rows, the first K/V rows of the split); the query
@@ -925,6 +830,11 @@ void step_gemvs(const egpt_qwen3_step* s, egpt_gemv_fused* out) {
 }
 
 }  // namespace
+
+size_t fused_step_bytes(const egpt_qwen3_step* s) { return step_layout(s).total; }
+int qwen3_check_step(const egpt_qwen3_step* s) { return check_step(s); }
+size_t persistent_step_bytes(const egpt_qwen3_step* s);  // qwen3_persistent.hip
+
 }  // namespace egpt
 
 using namespace egpt;
@@ -951,7 +861,8 @@ extern "C" int egpt_argmax_parts(const float* part_v, const int* part_i, int par
 extern "C" int egpt_qwen3_step_workspace(const egpt_qwen3_step* s, size_t* bytes) {
   if (!s || !bytes || s->heads < 1 || s->kv_heads < 1 || s->nsplit < 1 || s->head_dim < 1 || s->vocab < 1)
     return EGPT_ERR_INVALID;
-  *bytes = step_layout(s).total;
+  // the launch-per-phase step's region, then the persistent step's (qwen3_persistent.hip)
+  *bytes = (step_layout(s).total + 255) / 256 * 256 + persistent_step_bytes(s);
   return EGPT_OK;
 }
 

@@ -73,6 +73,9 @@ class GraphGreedyDecoder:
                                           or launched >= max_new_tokens):
                 events[emitted].synchronize()
                 tok = int(self.host[emitted])
+                if tok < 0:  # the persistent step's failure mark
+                    eng.check_status()
+                    raise RuntimeError('decode step reported a failure')
                 if first is None:
                     first = time.perf_counter()
                 out.append(tok)

@@ -37,6 +37,12 @@ from .int8_linear import MAX_DECODE_ROWS, int8_gemm, quantize_weight
 
 # Prompts longer than this take the library-GEMM attention in prefill.
 PREFILL_KERNEL_MAX_ROWS = 64
+# The persistent step attends with one block per kv head; longer caches keep the
+# launch-per-phase step, whose attention splits every kv head over many blocks.
+PERSISTENT_MAX_CACHE = 4096
+# Whether engines take the persistent step unless told otherwise: off while the
+# launch-per-phase step is the faster of the two on the MI355X.
+PERSISTENT_DEFAULT = False
 
 LINEARS = ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj', 'self_attn.o_proj',
            'mlp.gate_proj', 'mlp.up_proj', 'mlp.down_proj')
@@ -148,7 +154,7 @@ class Qwen3Int8Engine:
     the packed layout pack_qwen3 returns (what efficientgpt_amd.checkpoint stores).
     """
 
-    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False):
+    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False, persistent=None):
         if max_cache_len < 1:
             raise ValueError('max_cache_len must be >= 1')
         self.cfg, self.cap = cfg, int(max_cache_len)
@@ -195,7 +201,28 @@ class Qwen3Int8Engine:
         _lib.check('egpt_argmax_workspace', lib.egpt_argmax_workspace(c.vocab, need))
         self.arg_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
         self._build_step_desc()
+        self.persistent = self._choose_persistent(persistent)
         self.graph = None
+
+    def _choose_persistent(self, want):
+        """Whether step() is the one-launch persistent step (egpt_qwen3_persistent_step).
+
+        want True: required (raises if the library has no persistent kernel for this shape on this device);
+        None: when PERSISTENT_DEFAULT is set, the library supports it and the cache is short enough for its
+        one-split attention; False: the launch-per-phase step."""
+        if want is False or (want is None and not PERSISTENT_DEFAULT):
+            return False
+        lib = _lib.lib()
+        st = lib.egpt_qwen3_persistent_supported(ctypes.byref(self._step_c))
+        if st != _lib.EGPT_OK:
+            if want:
+                _lib.check('egpt_qwen3_persistent_supported', st)
+            return False
+        if want is None and self.cap > PERSISTENT_MAX_CACHE:
+            return False
+        _lib.check('egpt_qwen3_persistent_setup', lib.egpt_qwen3_persistent_setup(ctypes.byref(self._step_c),
+                                                                                  self._stream()))
+        return True
 
     def _build_step_desc(self):
         """The egpt_qwen3_step descriptor of the fused decode step (pointers into this engine's tensors)."""
@@ -231,15 +258,15 @@ class Qwen3Int8Engine:
     # ------------------------------------------------------------------ construction helpers
 
     @classmethod
-    def from_int8(cls, path, max_cache_len, device='cuda'):
+    def from_int8(cls, path, max_cache_len, device='cuda', persistent=None):
         """Engine over an efficientgpt_amd.checkpoint file: the stored int8 layout, no re-quantisation."""
         from .checkpoint import load_int8
         cfg, packed, inv_freq = load_int8(path)
-        return cls(cfg, packed, max_cache_len, device=device, inv_freq=inv_freq, packed=True)
+        return cls(cfg, packed, max_cache_len, device=device, inv_freq=inv_freq, packed=True, persistent=persistent)
 
     @classmethod
     @torch.no_grad()
-    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda'):
+    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda', persistent=None):
         """Random-init weights N(0, std) (bf16, norms 1), quantised per output channel on the device."""
         dev = torch.device(device)
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -269,7 +296,7 @@ class Qwen3Int8Engine:
             w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(randn(c.vocab, c.hidden))
         else:
             w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(w['model.embed_tokens.weight'])
-        eng = cls(cfg, w, max_cache_len, device=dev)
+        eng = cls(cfg, w, max_cache_len, device=dev, persistent=persistent)
         eng.weights = w  # kept so a CPU oracle can be built from the very same tensors
         return eng
 
@@ -393,9 +420,33 @@ class Qwen3Int8Engine:
     def step(self):
         """One decode step on the current stream: consumes self.token at self.position, writes the next token.
 
-        The fused step (egpt_qwen3_decode_step): five launches per layer and one for the head."""
+        The persistent step (one launch) when self.persistent, else the fused launch-per-phase step."""
+        if self.persistent:
+            self.step_persistent()
+        else:
+            self.step_fused()
+
+    @torch.inference_mode()
+    def step_fused(self):
+        """The fused step (egpt_qwen3_decode_step): five launches per layer and one for the head."""
         _lib.check('egpt_qwen3_decode_step', _lib.lib().egpt_qwen3_decode_step(ctypes.byref(self._step_c),
                                                                                self._stream()))
+
+    @torch.inference_mode()
+    def step_persistent(self):
+        """The whole step as one persistent launch (egpt_qwen3_persistent_step)."""
+        _lib.check('egpt_qwen3_persistent_step', _lib.lib().egpt_qwen3_persistent_step(ctypes.byref(self._step_c),
+                                                                                       self._stream()))
+
+    def check_status(self):
+        """Raise if any persistent step so far ran out a wait bound (synchronises with the device)."""
+        if not self.persistent:
+            return
+        st = ctypes.c_uint32()
+        _lib.check('egpt_qwen3_persistent_status', _lib.lib().egpt_qwen3_persistent_status(
+            ctypes.byref(self._step_c), ctypes.byref(st)))
+        if st.value:
+            raise RuntimeError(f'persistent decode step failed (status {st.value:#x}): a block waited past its bound')
 
     @torch.inference_mode()
     def step_unfused(self):
