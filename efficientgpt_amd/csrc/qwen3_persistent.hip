@@ -47,9 +47,9 @@
 // q/k norm, RoPE, residual, SwiGLU) and the int8 decode contract bf16(s * fp32 sum)
 // of research/realmodel/int8_linear.py:26-38; the attention is that of
 // research/phase5/decode_attention.py:22-71 over all live slots in one split. The
-// GEMV sums are fp32 sums of exact products, in the fp16-pair form of tile_sums().
-// The residual row a wavefront adds to stays in its registers from C to E to the
-// next layer's C.
+// GEMV rows are summed in the per-lane order and with the wavefront reduction of
+// the launch-per-phase kernels (step_core.h). The residual row a wavefront adds to
+// stays in its registers from C to E to the next layer's C.
 #include "step_core.h"
 
 #include <mutex>
@@ -221,21 +221,16 @@ __device__ __forceinline__ void poll_row(const uint32_t* src, int K, uint32_t ta
   }
 }
 
-// Stage a row in LDS for the GEMV tiles: the row's bf16 values h (RMS-normalised
-// when NORM: h = bf16(w * bf16(x * rsqrt(mean x^2 + eps)))) are scaled by 2^k and
-// stored as fp16 (hs[0 .. NCH * kPChunk), zero past K). k puts the row's largest
-// |h| just below 2^15, so every value within 2^-29 of it converts to fp16
-// exactly (a bf16 value has 8 significant bits, fp16 11) and none overflows;
-// smaller values lose bits as fp16 subnormals, below the fp32 accumulation's own
-// rounding. Returns 2^-k, which undoes the scaling of a finished dot product.
+// Stage a row in LDS as bf16 (hs[0 .. NCH * kPChunk), zero past K), RMS-normalised
+// when NORM: h = bf16(w * bf16(x * rsqrt(mean x^2 + eps))). The arithmetic and
+// its order are stage_finish()'s in qwen3_fused.hip.
 template <int NCH, bool NORM>
-__device__ __forceinline__ float stage_row(const Row<NCH>& x, const Row<NCH>& w, int K, float eps, uint16_t* hs) {
+__device__ __forceinline__ void stage_row(const Row<NCH>& x, const Row<NCH>& w, int K, float eps, uint16_t* hs) {
   constexpr int P = Row<NCH>::kPasses;
   const int tid = threadIdx.x;
   const u32x4 z{0u, 0u, 0u, 0u};
-  __shared__ float red[kPWaves];
-  u32x4 hb[P];  // bf16 values, zero past K
   if constexpr (NORM) {
+    __shared__ float red[kPWaves];
     float ss = 0.f;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -253,87 +248,32 @@ __device__ __forceinline__ float stage_row(const Row<NCH>& x, const Row<NCH>& w,
     const float inv = rsqrtf(total / (float)K + eps);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      hb[p] = z;
-      if (row_k8<NCH>(p) < K) {
-        float v[8], wv[8];
-        Elem<__bf16>::unpack(x.v[p], v);
-        Elem<__bf16>::unpack(w.v[p], wv);
-        uint32_t pk[4];
+      const int k8 = row_k8<NCH>(p);
+      if (k8 < NCH * kPChunk) {
+        u32x4 out = z;
+        if (k8 < K) {
+          float v[8], wv[8];
+          Elem<__bf16>::unpack(x.v[p], v);
+          Elem<__bf16>::unpack(w.v[p], wv);
+          uint32_t pk[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pk[e] = (uint32_t)f32_to_bf16(wv[2 * e] * bf16r(v[2 * e] * inv)) |
-                  ((uint32_t)f32_to_bf16(wv[2 * e + 1] * bf16r(v[2 * e + 1] * inv)) << 16);
-        hb[p] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+          for (int e = 0; e < 4; ++e)
+            pk[e] = (uint32_t)f32_to_bf16(wv[2 * e] * bf16r(v[2 * e] * inv)) |
+                    ((uint32_t)f32_to_bf16(wv[2 * e + 1] * bf16r(v[2 * e + 1] * inv)) << 16);
+          out = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        }
+        *(u32x4*)(hs + k8) = out;
       }
     }
-    lds_barrier();  // red[] is reused below
+    // red[] is reused by the next stage_row only after block_all()'s barriers
   } else {
 #pragma unroll
-    for (int p = 0; p < P; ++p) hb[p] = row_k8<NCH>(p) < K ? x.v[p] : z;
-  }
-  // the row's largest magnitude -> the scale
-  float mx = 0.f;
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    float v[8];
-    Elem<__bf16>::unpack(hb[p], v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
-  }
-  mx = wave_max(mx);
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = mx;
-  lds_barrier();
-  mx = red[0];
-#pragma unroll
-  for (int j = 1; j < kPWaves; ++j) mx = fmaxf(mx, red[j]);
-  const uint32_t ebits = (__float_as_uint(mx) >> 23) & 0xffu;  // mx < 2^(ebits - 126)
-  int k = (mx > 0.f && ebits != 0xffu) ? 15 - ((int)ebits - 126) : 0;
-  k = k < -100 ? -100 : (k > 100 ? 100 : k);
-  const float up = ldexpf(1.f, k);
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int k8 = row_k8<NCH>(p);
-    if (k8 < NCH * kPChunk) {
-      float v[8];
-      Elem<__bf16>::unpack(hb[p], v);
-      uint32_t pk[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        pk[e] = (uint32_t)f32_to_f16(v[2 * e] * up) | ((uint32_t)f32_to_f16(v[2 * e + 1] * up) << 16);
-      *(u32x4*)(hs + k8) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    for (int p = 0; p < P; ++p) {
+      const int k8 = row_k8<NCH>(p);
+      if (k8 < NCH * kPChunk) *(u32x4*)(hs + k8) = k8 < K ? x.v[p] : z;
     }
   }
   lds_barrier();
-  return ldexpf(1.f, -k);
-}
-
-// A wavefront's share of a staged row, held in registers across its tiles: the
-// 16 fp16 values of each 1 KiB chunk this lane multiplies (as 8 packed pairs) and
-// their sum (fp32, in chunk order).
-template <int NCH>
-struct XAct {
-  uint32_t xp[NCH][8];
-  float sx;
-};
-
-template <int NCH>
-__device__ __forceinline__ void load_act(const uint16_t* hs, int lane, XAct<NCH>& xa) {
-  xa.sx = 0.f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int k = c * kPChunk + lane * 16;
-    const u32x4 a = *(const u32x4*)(hs + k);
-    const u32x4 b = *(const u32x4*)(hs + k + 8);
-    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float ts = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      xa.xp[c][i] = u[i];
-      ts += f16_to_f32((uint16_t)(u[i] & 0xffffu));
-      ts += f16_to_f32((uint16_t)(u[i] >> 16));
-    }
-    xa.sx += ts;
-  }
 }
 
 // ------------------------------------------------------------------ GEMV tiles
@@ -387,38 +327,28 @@ __device__ __forceinline__ void tile_issue(PTile<R, NCH>& tl, const GDesc& g, in
   tl.sc2 = SWIGLU ? gload(g.scale + g.N + fc) : 0.f;
 }
 
-// Row totals of a tile (wave-uniform), times `down` (2^-k of the staged row).
-// Each 4 weight bytes are biased to unsigned (xor 0x80: u = w + 128) and become two
-// fp16 pairs by byte permutation, 0x6400 | u = 1024 + u = 1152 + w exactly; a
-// v_dot2_f32_f16 multiplies a pair by two activations and adds both products
-// (exact in fp32: 11 x 11 significant bits) to the fp32 sum. 1152 * sum(x) is
-// removed per lane before the wavefront reduction. Four instructions per four
-// weights, against eight for converting and multiplying each byte in fp32.
+// Row totals of a tile (wave-uniform), the activation from LDS: the per-lane
+// order and the reduction of stage_mac() + tile_finish() in qwen3_fused.hip.
 template <int R, int NCH>
-__device__ __forceinline__ void tile_sums(const PTile<R, NCH>& tl, const XAct<NCH>& xa, float down, float (&tot)[R]) {
-  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void tile_sums(const PTile<R, NCH>& tl, const uint16_t* hs, int lane, float (&tot)[R]) {
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  float sx = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
+    const int k = c * kPChunk + lane * 16;
+    float xf[16];
+    unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xf);
+    float ts = 0.f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const u32x4 wq = tl.w[c][r];
-      const uint32_t d[4] = {wq.x ^ 0x80808080u, wq.y ^ 0x80808080u, wq.z ^ 0x80808080u, wq.w ^ 0x80808080u};
+    for (int e = 0; e < 16; ++e) ts += xf[e];
+    sx += ts;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, d[j], 0x04010400u);  // bytes 0, 1
-        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, d[j], 0x04030402u);  // bytes 2, 3
-        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, lo), __builtin_bit_cast(half2_t, xa.xp[c][2 * j]),
-                                        acc[r], false);
-        acc[r] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, hi),
-                                        __builtin_bit_cast(half2_t, xa.xp[c][2 * j + 1]), acc[r], false);
-      }
-    }
+    for (int r = 0; r < R; ++r) acc[r] = dot16_biased(tl.w[c][r], xf, acc[r]);
   }
 #pragma unroll
-  for (int r = 0; r < R; ++r) tot[r] = wave_sum(acc[r] - 1152.f * xa.sx) * down;
+  for (int r = 0; r < R; ++r) tot[r] = wave_sum(acc[r] - 128.f * sx);
 }
 
 // The value of row r < R that lane `lane` stores (lane r of the tile).
@@ -542,9 +472,7 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
   bool broken = false;
   auto tiles_of = [&](int ntiles, int w, int tw) { return w < ntiles ? (ntiles - w + tw - 1) / tw : 0; };
 
-  float down;
   if (role == 0) {
-    XAct<NH> xh;
     const int TA = tiles_of((nqkv + 1) / 2, gw, TW);
     const int TD = tiles_of(a.inter, gw, TW);
     PTile<2, NH> tA[PFA];
@@ -563,13 +491,12 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
         load_row<NH>(L.in_norm, a.hidden, w);
         if (i == 0) load_row<NH>(erow, a.hidden, x);
         else poll_row<NH>(a.xa, a.hidden, tag(id - 1), x, broken);
-        down = stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
+        stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
       }
-      load_act<NH>(hs, lane, xh);
 #pragma unroll
       for (int j = 0; j < PFA; ++j) {
         float tot[2];
-        tile_sums<2, NH>(tA[j], xh, down, tot);
+        tile_sums<2, NH>(tA[j], hs, lane, tot);
         const int f = (gw + j * TW) * 2 + lane;
         if (lane < 2 && j < TA && f < nqkv)
           tag_store(a.qkv + f, tag(id), f32_to_bf16(lane_pick<2>(tot, lane) * tA[j].sc));
@@ -583,13 +510,12 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
         Row<NH> x, w;
         load_row<NH>(L.post_norm, a.hidden, w);
         poll_row<NH>(a.xb, a.hidden, tag(id + 2), x, broken);
-        down = stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
+        stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
       }
-      load_act<NH>(hs, lane, xh);
 #pragma unroll
       for (int j = 0; j < PFD; ++j) {
         float tot[2];
-        tile_sums<2, NH>(tD[j], xh, down, tot);
+        tile_sums<2, NH>(tD[j], hs, lane, tot);
         const int f = gw + j * TW;
         if (lane == 0 && j < TD && f < a.inter) {
           const float g = bf16r(tot[0] * tD[j].sc);
@@ -627,15 +553,13 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
       {
         Row<NO> x;
         poll_row<NO>(a.attn, Hq * D, tag(id + 1), x, broken);
-        down = stage_row<NO, false>(x, x, Hq * D, a.eps, hs);
+        stage_row<NO, false>(x, x, Hq * D, a.eps, hs);
       }
       {
-        XAct<NO> xo;
-        load_act<NO>(hs, lane, xo);
 #pragma unroll
         for (int j = 0; j < PFC; ++j) {
           float tot[1];
-          tile_sums<1, NO>(tC[j], xo, down, tot);
+          tile_sums<1, NO>(tC[j], hs, lane, tot);
         const int f = gw + j * TW;
         if (lane == 0 && j < TC && f < a.hidden) {
           const uint16_t xn = f32_to_bf16(res[j] + bf16r(tot[0] * tC[j].sc));
@@ -652,15 +576,13 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
       {
         Row<NI> x;
         poll_row<NI>(a.act, a.inter, tag(id + 3), x, broken);
-        down = stage_row<NI, false>(x, x, a.inter, a.eps, hs);
+        stage_row<NI, false>(x, x, a.inter, a.eps, hs);
       }
       {
-        XAct<NI> xi;
-        load_act<NI>(hs, lane, xi);
 #pragma unroll
         for (int j = 0; j < PFE; ++j) {
           float tot[1];
-          tile_sums<1, NI>(tE[j], xi, down, tot);
+          tile_sums<1, NI>(tE[j], hs, lane, tot);
         const int f = gw + j * TW;
         if (lane == 0 && j < TC && f < a.hidden) {
           const uint16_t xn = f32_to_bf16(res[j] + bf16r(tot[0] * tE[j].sc));
@@ -691,17 +613,32 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
     Row<NH> x, w;
     load_row<NH>(a.final_norm, a.hidden, w);
     poll_row<NH>(a.xa, a.hidden, tag(idh - 1), x, broken);
-    down = stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
+    stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
   }
-  XAct<NH> xq;
-  load_act<NH>(hs, lane, xq);
+  // the activation and its sum stay in registers across the tiles (the order of
+  // the launch-per-phase lm_head)
+  float xh[NH][16];
+  float sxh = 0.f;
+#pragma unroll
+  for (int c = 0; c < NH; ++c) {
+    const int k = c * kPChunk + lane * 16;
+    unpack_bf16x16(*(const u32x4*)(hs + k), *(const u32x4*)(hs + k + 8), xh[c]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sxh += xh[c][e];
+  }
   ArgBest best{-INFINITY, 0x7fffffff};
   for (int j0 = 0; j0 < TH; j0 += PFH) {
 #pragma unroll
     for (int s = 0; s < PFH; ++s) {
       const int j = j0 + s;
+      float acc[2] = {0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NH; ++c)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) acc[r] = dot16_biased(tH[s].w[c][r], xh[c], acc[r]);
       float tot[2];
-      tile_sums<2, NH>(tH[s], xq, down, tot);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) tot[r] = wave_sum(acc[r] - 128.f * sxh);
       const int f = (gwh + j * TWH) * 2 + lane;
       if (lane < 2 && j < TH && f < a.vocab) {
         const uint16_t lg = f32_to_bf16(lane_pick<2>(tot, lane) * tH[s].sc);
