@@ -1,18 +1,22 @@
 // Persistent batch-1 Qwen3 decode step on gfx950 (MI355X): the whole step, every
-// layer and the head, as ONE launch of two 4-wavefront blocks per CU.
+// layer and the head, as ONE launch of one 8-wavefront block per CU.
 //
 // The launch-per-phase step (qwen3_fused.hip) pays a kernel boundary (about 1.5 us)
-// between each of its 142 dependent launches. Here the blocks stay resident and
-// hand rows to each other through device memory; a block stores a phase's
-// outputs, issues the weight loads of its next phase and only then waits for that
-// phase's input, so the stream overlaps the hand-off. (Issuing the loads before
-// the current phase's arithmetic would delay it: a wavefront's load issue stalls
+// between each of its 142 dependent launches, and each small launch pays its own
+// start-up and drain. Here the blocks stay resident and hand rows to each other
+// through device memory. A hand-off costs about as much as a launch boundary
+// (measured 2.0 us across 256 blocks), but the next phase's weights stream while
+// it happens: every wavefront stores its outputs, then issues the loads of its
+// next GEMV tiles, then waits for that GEMV's input row. (Issuing them before the
+// current phase's arithmetic would delay it: a wavefront's load issue stalls
 // until the memory system has room, about as long as the stream itself.)
 //
 // Measured on the MI355X this form is slower than the launch-per-phase step
-// (about 1.1-1.2 ms against 0.75 ms per Qwen3-1.7B token): a hand-off costs 2 us
-// on an idle chip but 4-6 us while the weight streams are in flight, more than
-// the launch boundary it replaces. It is kept as a tested alternative.
+// (about 0.93 against 0.75 ms per Qwen3-1.7B token): a hand-off costs 2 us on an
+// idle chip but 3-6 us while the weight streams are in flight, more than the
+// launch boundary it replaces, and each phase's arithmetic (about 0.6 us per
+// two-row tile: a wave64 issues one VALU instruction per 4 cycles) runs after
+// its hand-off instead of under a stream. It is kept as a tested alternative.
 //
 // Hand-off protocol (no fences, no counters). Every row one phase passes to the
 // next is stored as 32-bit words (tag << 16) | bf16 bits with agent-scope relaxed
@@ -30,26 +34,27 @@
 // Every wait is bounded: a block whose poll runs past kMaxPolls stops waiting for
 // the rest of the step (its results are then meaningless), the step stores token
 // -1 and sets bit 0 of the workspace status word, and the launch still ends. The
-// grid is two blocks per CU, within what the occupancy query says fits at once,
+// grid is one block per CU, within what the occupancy query says fits at once,
 // so every block is resident and every producer runs.
 //
-// Per layer i (5 phases; role 0 = blocks b with (b / 8) even, role 1 the others):
-//   A  role 0: RMSNorm(x; input_layernorm) -> QKV GEMV     -> qkv   (layer 0: x = embedding[token])
-//   B  role 1, its blocks 0..kv_heads-1: q/k RMSNorm + RoPE, K/V slot p write,
-//      attention over slots 0..p, one block per kv head    -> attn
-//   C  role 1: o_proj GEMV(attn) + residual                 -> x (xb)
-//   D  role 0: RMSNorm(x; post_attention_layernorm) -> gate/up GEMV -> SwiGLU -> act
-//   E  role 1: down GEMV(act) + residual                    -> x (xa)
-// Head (both roles): RMSNorm(x; norm) -> lm_head GEMV -> per-block argmax -> block 0
-// picks the token, advances the position and the epoch.
+// Per layer i (5 phases; rows are split over all 8 * CUs wavefronts):
+//   A  RMSNorm(x; input_layernorm) -> QKV GEMV             -> qkv   (layer 0: x = embedding[token])
+//   B  blocks 0..kv_heads-1: q/k RMSNorm + RoPE, K/V slot p write, attention over
+//      slots 0..p, one block per kv head (its 8 wavefronts split the slots) -> attn
+//   C  o_proj GEMV(attn) + residual                           -> x (xb)
+//   D  RMSNorm(x; post_attention_layernorm) -> gate/up GEMV -> SwiGLU -> act
+//   E  down GEMV(act) + residual                              -> x (xa)
+// Head: RMSNorm(x; norm) -> lm_head GEMV -> per-block argmax -> block 0 picks the
+// token, advances the position and the epoch.
 //
-// Roundings are transformers' bf16 Qwen3 (models/qwen3/modeling_qwen3.py: RMSNorm,
-// q/k norm, RoPE, residual, SwiGLU) and the int8 decode contract bf16(s * fp32 sum)
-// of research/realmodel/int8_linear.py:26-38; the attention is that of
-// research/phase5/decode_attention.py:22-71 over all live slots in one split. The
-// GEMV rows are summed in the per-lane order and with the wavefront reduction of
-// the launch-per-phase kernels (step_core.h). The residual row a wavefront adds to
-// stays in its registers from C to E to the next layer's C.
+// Arithmetic is that of the launch-per-phase step, from the same device functions
+// (step_core.h): GEMV rows in the same per-lane order with the same wavefront
+// reduction, RMSNorm / RoPE / residual / SwiGLU roundings of transformers' bf16
+// Qwen3 (models/qwen3/modeling_qwen3.py), the int8 decode contract
+// bf16(s * fp32 sum) of research/realmodel/int8_linear.py:26-38, and the
+// attention of research/phase5/decode_attention.py:22-71 over all live slots in
+// one split. The residual row a wavefront adds to stays in its registers from C
+// to E to the next layer's C.
 #include "step_core.h"
 
 #include <mutex>
@@ -62,7 +67,7 @@ int qwen3_check_step(const egpt_qwen3_step* s);     // qwen3_fused.hip
 
 namespace {
 
-constexpr int kPWaves = 4;
+constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * kWave;
 constexpr int kPChunk = kWave * 16;       // int8 weights of one 16-byte load per lane
 constexpr uint32_t kOOB = 0x80000000u;    // buffer offset past every weight matrix (host-checked)
@@ -430,19 +435,11 @@ __device__ __forceinline__ void attention_block(const PArgs& a, const PLayer& L,
 
 // ------------------------------------------------------------------ the step
 
-// Two roles of 4-wavefront blocks, two blocks per CU: role 0 runs phases A (QKV)
-// and D (gate/up); role 1 runs B (attention, on its blocks 0..kv_heads-1), C
-// (o_proj) and E (down). A block stores a phase's outputs, issues the weight loads
-// of its next phase and only then waits for that phase's input: in between, the
-// other role runs a phase and two hand-offs, which hides the stream. Blocks
-// alternate roles in runs of 8 (block b has role (b / 8) % 2), so each role is
-// spread over every XCD.
-//
 // NH / NI / NO: 1 KiB chunks of the hidden, intermediate and attention rows;
-// G: query heads per kv head; PFA/PFC/PFD/PFE: tiles per wavefront of phases A,
-// C, D, E, all held in registers (the host checks that they fit); PFH: the
-// head's ring of tiles.
-template <int NH, int NI, int NO, int G, int PFA, int PFC, int PFD, int PFE, int PFH>
+// G: query heads per kv head; PFA/PFC/PFD/PFE: tiles per wavefront held in
+// registers for phases A, C, D, E (the host checks that every wavefront's tiles
+// fit, except D with STREAM_D, which refills its ring); PFH: the head's ring.
+template <int NH, int NI, int NO, int G, int PFA, int PFC, int PFD, int PFE, int PFH, bool STREAM_D>
 __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs a) {
   static_assert(PFC == PFE, "C and E keep one residual per tile");
   constexpr int D = kHeadDim;
@@ -452,11 +449,8 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int b = (int)blockIdx.x;
-  const int role = (b >> 3) & 1;
-  const int rb = ((b >> 4) << 3) | (b & 7);  // block index within the role
-  const int TW = (int)(gridDim.x / 2) * kPWaves;  // wavefronts per role
-  const int gw = rb * kPWaves + wave;
+  const int TW = (int)gridDim.x * kPWaves;
+  const int gw = (int)blockIdx.x * kPWaves + wave;
   const int Hkv = a.kv_heads;
   const int Hq = a.heads;
   const int nqkv = (Hq + 2 * Hkv) * D;
@@ -470,145 +464,135 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
   tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
   const uint16_t* erow = a.embed + tok * a.hidden;
   bool broken = false;
-  auto tiles_of = [&](int ntiles, int w, int tw) { return w < ntiles ? (ntiles - w + tw - 1) / tw : 0; };
 
-  if (role == 0) {
-    const int TA = tiles_of((nqkv + 1) / 2, gw, TW);
-    const int TD = tiles_of(a.inter, gw, TW);
-    PTile<2, NH> tA[PFA];
+  auto tiles_of = [&](int ntiles) { return gw < ntiles ? (ntiles - gw + TW - 1) / TW : 0; };
+  const int TA = tiles_of((nqkv + 1) / 2);
+  const int TC = tiles_of(a.hidden);
+  const int TD = tiles_of(a.inter);
+
+  // residual rows (lane 0 of each C/E tile): layer 0 adds to the embedding row
+  float res[PFC];
+#pragma unroll
+  for (int j = 0; j < PFC; ++j) res[j] = bf16_to_f32(gload(erow + min(gw + j * TW, a.hidden - 1)));
+
+  PTile<2, NH> tA[PFA];
+  {
+    const PLayer L0 = read_layer(a.tab, 0);
+    const GDesc gA = gdesc(L0.qkv_w, L0.qkv_s, nqkv, a.hidden, nqkv, 2);
+#pragma unroll
+    for (int j = 0; j < PFA; ++j) tile_issue<2, NH, false>(tA[j], gA, gw + j * TW, lane);
+  }
+
+  for (int i = 0; i < a.layers; ++i) {
+    const PLayer L = read_layer(a.tab, i);
+    const int id = i * kPhasesPerLayer;
+
+    // ---- A: RMSNorm -> QKV
     {
-      const PLayer L0 = read_layer(a.tab, 0);
-      const GDesc gA = gdesc(L0.qkv_w, L0.qkv_s, nqkv, a.hidden, nqkv, 2);
-#pragma unroll
-      for (int j = 0; j < PFA; ++j) tile_issue<2, NH, false>(tA[j], gA, gw + j * TW, lane);
+      Row<NH> x, w;
+      load_row<NH>(L.in_norm, a.hidden, w);
+      if (i == 0) load_row<NH>(erow, a.hidden, x);
+      else poll_row<NH>(a.xa, a.hidden, tag(id - 1), x, broken);
+      stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
     }
-    for (int i = 0; i < a.layers; ++i) {
-      const PLayer L = read_layer(a.tab, i);
-      const int id = i * kPhasesPerLayer;
-      // ---- A: RMSNorm -> QKV
-      {
-        Row<NH> x, w;
-        load_row<NH>(L.in_norm, a.hidden, w);
-        if (i == 0) load_row<NH>(erow, a.hidden, x);
-        else poll_row<NH>(a.xa, a.hidden, tag(id - 1), x, broken);
-        stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
-      }
 #pragma unroll
-      for (int j = 0; j < PFA; ++j) {
+    for (int j = 0; j < PFA; ++j) {
+      float tot[2];
+      tile_sums<2, NH>(tA[j], hs, lane, tot);
+      const int f = (gw + j * TW) * 2 + lane;
+      if (lane < 2 && j < TA && f < nqkv) tag_store(a.qkv + f, tag(id), f32_to_bf16(lane_pick<2>(tot, lane) * tA[j].sc));
+    }
+    PTile<1, NO> tC[PFC];
+    const GDesc gC = gdesc(L.o_w, L.o_s, a.hidden, Hq * D, a.hidden, 1);
+#pragma unroll
+    for (int j = 0; j < PFC; ++j) tile_issue<1, NO, false>(tC[j], gC, gw + j * TW, lane);
+
+    // ---- B: attention, one block per kv head
+    if ((int)blockIdx.x < Hkv) attention_block<G>(a, L, (int)blockIdx.x, pos, tag(id), tag(id + 1), broken);
+
+    // ---- C: o_proj + residual -> xb
+    {
+      Row<NO> x;
+      poll_row<NO>(a.attn, Hq * D, tag(id + 1), x, broken);
+      stage_row<NO, false>(x, x, Hq * D, a.eps, hs);
+    }
+#pragma unroll
+    for (int j = 0; j < PFC; ++j) {
+      float tot[1];
+      tile_sums<1, NO>(tC[j], hs, lane, tot);
+      const int f = gw + j * TW;
+      if (lane == 0 && j < TC && f < a.hidden) {
+        const uint16_t xn = f32_to_bf16(res[j] + bf16r(tot[0] * tC[j].sc));
+        tag_store(a.xb + f, tag(id + 2), xn);
+        res[j] = bf16_to_f32(xn);
+      }
+    }
+    PTile<2, NH> tD[PFD];
+    const GDesc gD = gdesc(L.gu_w, L.gu_s, a.inter, a.hidden, 2 * a.inter, 1);
+#pragma unroll
+    for (int j = 0; j < PFD; ++j) tile_issue<2, NH, true>(tD[j], gD, gw + j * TW, lane);
+
+    // ---- D: RMSNorm -> gate/up -> SwiGLU -> act
+    {
+      Row<NH> x, w;
+      load_row<NH>(L.post_norm, a.hidden, w);
+      poll_row<NH>(a.xb, a.hidden, tag(id + 2), x, broken);
+      stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
+    }
+    for (int j0 = 0; j0 < TD; j0 += PFD) {
+#pragma unroll
+      for (int s = 0; s < PFD; ++s) {
+        const int j = j0 + s;
         float tot[2];
-        tile_sums<2, NH>(tA[j], hs, lane, tot);
-        const int f = (gw + j * TW) * 2 + lane;
-        if (lane < 2 && j < TA && f < nqkv)
-          tag_store(a.qkv + f, tag(id), f32_to_bf16(lane_pick<2>(tot, lane) * tA[j].sc));
-      }
-      PTile<2, NH> tD[PFD];
-      const GDesc gD = gdesc(L.gu_w, L.gu_s, a.inter, a.hidden, 2 * a.inter, 1);
-#pragma unroll
-      for (int j = 0; j < PFD; ++j) tile_issue<2, NH, true>(tD[j], gD, gw + j * TW, lane);
-      // ---- D: RMSNorm -> gate/up -> SwiGLU -> act
-      {
-        Row<NH> x, w;
-        load_row<NH>(L.post_norm, a.hidden, w);
-        poll_row<NH>(a.xb, a.hidden, tag(id + 2), x, broken);
-        stage_row<NH, true>(x, w, a.hidden, a.eps, hs);
-      }
-#pragma unroll
-      for (int j = 0; j < PFD; ++j) {
-        float tot[2];
-        tile_sums<2, NH>(tD[j], hs, lane, tot);
+        tile_sums<2, NH>(tD[s], hs, lane, tot);
         const int f = gw + j * TW;
         if (lane == 0 && j < TD && f < a.inter) {
-          const float g = bf16r(tot[0] * tD[j].sc);
-          const float u = bf16r(tot[1] * tD[j].sc2);
+          const float g = bf16r(tot[0] * tD[s].sc);
+          const float u = bf16r(tot[1] * tD[s].sc2);
           const float sg = bf16r(g / (1.0f + expf(-g)));
           tag_store(a.act + f, tag(id + 3), f32_to_bf16(sg * u));
         }
+        if constexpr (STREAM_D) tile_issue<2, NH, true>(tD[s], gD, gw + (j + PFD) * TW, lane);
       }
-      if (i + 1 < a.layers) {
-        const PLayer Ln = read_layer(a.tab, i + 1);
-        const GDesc gA = gdesc(Ln.qkv_w, Ln.qkv_s, nqkv, a.hidden, nqkv, 2);
-#pragma unroll
-        for (int j = 0; j < PFA; ++j) tile_issue<2, NH, false>(tA[j], gA, gw + j * TW, lane);
-      }
+      if constexpr (!STREAM_D) break;
     }
-  } else {
-    const int TC = tiles_of(a.hidden, gw, TW);
-    // residual rows (lane 0 of each C/E tile): layer 0 adds to the embedding row
-    float res[PFC];
+    PTile<1, NI> tE[PFE];
+    const GDesc gE = gdesc(L.down_w, L.down_s, a.hidden, a.inter, a.hidden, 1);
 #pragma unroll
-    for (int j = 0; j < PFC; ++j) res[j] = bf16_to_f32(gload(erow + min(gw + j * TW, a.hidden - 1)));
-    PTile<1, NO> tC[PFC];
+    for (int j = 0; j < PFE; ++j) tile_issue<1, NI, false>(tE[j], gE, gw + j * TW, lane);
+
+    // ---- E: down + residual -> xa
     {
-      const PLayer L0 = read_layer(a.tab, 0);
-      const GDesc gC = gdesc(L0.o_w, L0.o_s, a.hidden, Hq * D, a.hidden, 1);
-#pragma unroll
-      for (int j = 0; j < PFC; ++j) tile_issue<1, NO, false>(tC[j], gC, gw + j * TW, lane);
+      Row<NI> x;
+      poll_row<NI>(a.act, a.inter, tag(id + 3), x, broken);
+      stage_row<NI, false>(x, x, a.inter, a.eps, hs);
     }
-    for (int i = 0; i < a.layers; ++i) {
-      const PLayer L = read_layer(a.tab, i);
-      const int id = i * kPhasesPerLayer;
-      // ---- B: attention, one block per kv head
-      if (rb < Hkv) attention_block<G>(a, L, rb, pos, tag(id), tag(id + 1), broken);
-      // ---- C: o_proj + residual -> xb
-      {
-        Row<NO> x;
-        poll_row<NO>(a.attn, Hq * D, tag(id + 1), x, broken);
-        stage_row<NO, false>(x, x, Hq * D, a.eps, hs);
-      }
-      {
 #pragma unroll
-        for (int j = 0; j < PFC; ++j) {
-          float tot[1];
-          tile_sums<1, NO>(tC[j], hs, lane, tot);
-        const int f = gw + j * TW;
-        if (lane == 0 && j < TC && f < a.hidden) {
-          const uint16_t xn = f32_to_bf16(res[j] + bf16r(tot[0] * tC[j].sc));
-          tag_store(a.xb + f, tag(id + 2), xn);
-          res[j] = bf16_to_f32(xn);
-          }
-        }
+    for (int j = 0; j < PFE; ++j) {
+      float tot[1];
+      tile_sums<1, NI>(tE[j], hs, lane, tot);
+      const int f = gw + j * TW;
+      if (lane == 0 && j < TC && f < a.hidden) {
+        const uint16_t xn = f32_to_bf16(res[j] + bf16r(tot[0] * tE[j].sc));
+        tag_store(a.xa + f, tag(id + 4), xn);
+        res[j] = bf16_to_f32(xn);
       }
-      PTile<1, NI> tE[PFE];
-      const GDesc gE = gdesc(L.down_w, L.down_s, a.hidden, a.inter, a.hidden, 1);
+    }
+    if (i + 1 < a.layers) {
+      const PLayer Ln = read_layer(a.tab, i + 1);
+      const GDesc gA = gdesc(Ln.qkv_w, Ln.qkv_s, nqkv, a.hidden, nqkv, 2);
 #pragma unroll
-      for (int j = 0; j < PFE; ++j) tile_issue<1, NI, false>(tE[j], gE, gw + j * TW, lane);
-      // ---- E: down + residual -> xa
-      {
-        Row<NI> x;
-        poll_row<NI>(a.act, a.inter, tag(id + 3), x, broken);
-        stage_row<NI, false>(x, x, a.inter, a.eps, hs);
-      }
-      {
-#pragma unroll
-        for (int j = 0; j < PFE; ++j) {
-          float tot[1];
-          tile_sums<1, NI>(tE[j], hs, lane, tot);
-        const int f = gw + j * TW;
-        if (lane == 0 && j < TC && f < a.hidden) {
-          const uint16_t xn = f32_to_bf16(res[j] + bf16r(tot[0] * tE[j].sc));
-          tag_store(a.xa + f, tag(id + 4), xn);
-          res[j] = bf16_to_f32(xn);
-          }
-        }
-      }
-      if (i + 1 < a.layers) {
-        const PLayer Ln = read_layer(a.tab, i + 1);
-        const GDesc gC = gdesc(Ln.o_w, Ln.o_s, a.hidden, Hq * D, a.hidden, 1);
-#pragma unroll
-        for (int j = 0; j < PFC; ++j) tile_issue<1, NO, false>(tC[j], gC, gw + j * TW, lane);
-      }
+      for (int j = 0; j < PFA; ++j) tile_issue<2, NH, false>(tA[j], gA, gw + j * TW, lane);
     }
   }
 
-  // ---- head: RMSNorm -> lm_head -> per-block argmax, both roles (wavefronts over the whole grid)
+  // ---- head: RMSNorm -> lm_head -> per-block argmax
   const int idh = a.layers * kPhasesPerLayer;
   const GDesc gH = gdesc(a.head_w, a.head_s, a.vocab, a.hidden, a.vocab, 2);
-  const int TWH = (int)gridDim.x * kPWaves;
-  const int gwh = b * kPWaves + wave;
-  const int TH = tiles_of(gH.ntiles, gwh, TWH);
+  const int TH = tiles_of(gH.ntiles);
   PTile<2, NH> tH[PFH];
 #pragma unroll
-  for (int s = 0; s < PFH; ++s) tile_issue<2, NH, false>(tH[s], gH, gwh + s * TWH, lane);
+  for (int s = 0; s < PFH; ++s) tile_issue<2, NH, false>(tH[s], gH, gw + s * TW, lane);
   {
     Row<NH> x, w;
     load_row<NH>(a.final_norm, a.hidden, w);
@@ -639,13 +623,13 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
       float tot[2];
 #pragma unroll
       for (int r = 0; r < 2; ++r) tot[r] = wave_sum(acc[r] - 128.f * sxh);
-      const int f = (gwh + j * TWH) * 2 + lane;
+      const int f = (gw + j * TW) * 2 + lane;
       if (lane < 2 && j < TH && f < a.vocab) {
         const uint16_t lg = f32_to_bf16(lane_pick<2>(tot, lane) * tH[s].sc);
         if (a.logits) gstore(a.logits + f, lg);
         best = arg_better(best, ArgBest{bf16_to_f32(lg), f});
       }
-      tile_issue<2, NH, false>(tH[s], gH, gwh + (j + PFH) * TWH, lane);
+      tile_issue<2, NH, false>(tH[s], gH, gw + (j + PFH) * TW, lane);
     }
   }
   best = block_argbest<kPWaves>(best);
@@ -665,9 +649,9 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
     bool ok = true;
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int pb = u * kPThreads + tid;
-      const bool in = pb < (int)gridDim.x;
-      words[u] = __hip_atomic_load((global_ptr<uint64_t>)(a.argp + (in ? pb : 0)), __ATOMIC_RELAXED,
+      const int b = u * kPThreads + tid;
+      const bool in = b < (int)gridDim.x;
+      words[u] = __hip_atomic_load((global_ptr<uint64_t>)(a.argp + (in ? b : 0)), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
       ok = ok && (!in || ((uint32_t)words[u] >> 19) == tagh);
     }
@@ -682,8 +666,8 @@ __global__ __launch_bounds__(kPThreads) void qwen3_persistent_kernel(const PArgs
   bool any_broken = broken;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
-    const int pb = u * kPThreads + tid;
-    if (pb < (int)gridDim.x) {
+    const int b = u * kPThreads + tid;
+    if (b < (int)gridDim.x) {
       const uint32_t lo = (uint32_t)words[u];
       const uint32_t idx = lo & kNoIndex;
       any_broken = any_broken || ((lo >> 18) & 1u);
@@ -740,6 +724,7 @@ typedef void (*PKernel)(PArgs);
 struct PVariant {
   PKernel kernel;
   int pfa, pfc, pfd, pfe;
+  bool stream_d;
 };
 
 bool variant_for(const egpt_qwen3_step* s, PVariant& v) {
@@ -747,7 +732,7 @@ bool variant_for(const egpt_qwen3_step* s, PVariant& v) {
   if (s->head_dim != kHeadDim) return false;
   if (s->hidden == 2048 && s->inter == 6144 && s->heads * s->head_dim == 2048 && g == 2) {
     // Qwen3-1.7B
-    v = PVariant{qwen3_persistent_kernel<2, 6, 2, 2, 2, 2, 6, 2, 4>, 2, 2, 6, 2};
+    v = PVariant{qwen3_persistent_kernel<2, 6, 2, 2, 1, 1, 3, 1, 4, false>, 1, 1, 3, 1, false};
     return true;
   }
   return false;
@@ -805,14 +790,13 @@ int persistent_check(const egpt_qwen3_step* s, PVariant& v, int& grid) {
   DevInfo d;
   const int di = device_info(v, d);
   if (di != EGPT_OK) return di;
-  // two blocks of each CU, one per role; 8-block runs alternate roles
-  grid = 2 * d.cus;
-  if (d.cus % 8 || d.cus < s->kv_heads || grid > kMaxGrid || d.occupancy < 2) return EGPT_ERR_UNSUPPORTED;
-  const int64_t tw = (int64_t)d.cus * kPWaves;  // wavefronts per role
+  grid = d.cus;
+  if (grid < s->kv_heads || grid > kMaxGrid || d.occupancy < 1) return EGPT_ERR_UNSUPPORTED;
+  const int64_t tw = (int64_t)grid * kPWaves;
   auto per_wave = [&](int64_t tiles) { return (tiles + tw - 1) / tw; };
   const int64_t nqkv = (int64_t)(s->heads + 2 * s->kv_heads) * s->head_dim;
   if (per_wave((nqkv + 1) / 2) > v.pfa || per_wave(s->hidden) > v.pfc || per_wave(s->hidden) > v.pfe ||
-      per_wave(s->inter) > v.pfd)
+      (!v.stream_d && per_wave(s->inter) > v.pfd))
     return EGPT_ERR_UNSUPPORTED;
   const int64_t lim = kOOB;
   if ((int64_t)s->vocab * s->hidden >= lim || (int64_t)2 * s->inter * s->hidden >= lim || nqkv * s->hidden >= lim ||

@@ -279,7 +279,7 @@ int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
 int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
 
 /*
- * The same decode step as ONE persistent launch (two 4-wavefront blocks per CU):
+ * The same decode step as ONE persistent launch (one 8-wavefront block per CU):
  * the blocks stay resident for the whole step and hand each phase's rows to the
  * next through epoch-tagged words in the workspace, each wavefront streaming its
  * next GEMV tiles while it waits. On the MI355X it is slower than
