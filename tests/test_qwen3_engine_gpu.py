@@ -99,10 +99,11 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
     assert agree / total >= 0.95, agree / total
 
 
-@pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048)])
+@pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048), (TINY, 0.2, 4096)])
 def test_fused_step_matches_unfused_step(shape, std, cap):
     """The fused step against the one-kernel-per-op step on the same tokens. cap 96 merges the
-    attention splits inside the o_proj GEMV; cap 2048 (32 splits) takes the separate merge launch."""
+    attention splits inside the o_proj GEMV; cap 2048 (32 splits) and TINY at cap 4096 (2 kv heads, 64 splits)
+    take the separate merge launch."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(3))
     runs = {}
