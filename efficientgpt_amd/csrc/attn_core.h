@@ -304,21 +304,30 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
   }
 
   // Merge the groups of each wavefront: butterflies across groups (lane
-  // distance LPS, 2*LPS, ...). Both partners end with the merged state.
+  // distance LPS, 2*LPS, ...). Both partners end with the same merged state: at
+  // distances 16 and 32 each value arrives as the (lower, upper) partner pair
+  // (pair16 / pair32) and both lanes combine them in that order.
 #pragma unroll
   for (int off = LPS; off < kWave; off *= 2) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float mo = __shfl_xor(m[g], off, kWave);
-      const float lo = __shfl_xor(l[g], off, kWave);
-      const float mx = fmaxf(m[g], mo);
-      const float ws = mx == -INFINITY ? 0.f : exp2f((m[g] - mx) * kLog2e);
-      const float wo = mx == -INFINITY ? 0.f : exp2f((mo - mx) * kLog2e);
-      l[g] = l[g] * ws + lo * wo;
+      auto pair = [&](float v) -> LanePair {
+        if (off == 16) return pair16(v);
+        if (off == 32) return pair32(v);
+        const float o = __shfl_xor(v, off, kWave);
+        const bool upper = (threadIdx.x & off) != 0;
+        return upper ? LanePair{o, v} : LanePair{v, o};
+      };
+      const LanePair mp = pair(m[g]);
+      const LanePair lp = pair(l[g]);
+      const float mx = fmaxf(mp.lo, mp.hi);
+      const float wl = mx == -INFINITY ? 0.f : exp2f((mp.lo - mx) * kLog2e);
+      const float wh = mx == -INFINITY ? 0.f : exp2f((mp.hi - mx) * kLog2e);
+      l[g] = lp.lo * wl + lp.hi * wh;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        const float ao = __shfl_xor(acc[g][e], off, kWave);
-        acc[g][e] = acc[g][e] * ws + ao * wo;
+        const LanePair ap = pair(acc[g][e]);
+        acc[g][e] = ap.lo * wl + ap.hi * wh;
       }
       m[g] = mx;
     }

@@ -102,6 +102,27 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
 constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
 
+constexpr int kDppRowRor8 = 0x128;    // lane i <- lane (i + 8) mod 16 within 16 lanes: xor 8
+
+// The values of lanes l and l ^ 16 (resp. l ^ 32) as (lower partner, upper
+// partner), the same pair on both lanes: one v_permlane16_swap / v_permlane32_swap
+// (gfx950) instead of an LDS-crossbar shuffle. A symmetric combine of the two
+// (sum, max, the softmax merge) computed as f(lo, hi) is then bit-identical on
+// both partners.
+struct LanePair {
+  float lo, hi;
+};
+__device__ __forceinline__ LanePair pair16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return LanePair{__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+__device__ __forceinline__ LanePair pair32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return LanePair{__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+// The value of lane l ^ 8 (16-lane rows: a DPP row rotation by 8).
+__device__ __forceinline__ float xor8(float v) { return dpp<kDppRowRor8>(v); }
+
 // Sum over aligned groups of N lanes (N in 1,2,4,8,16,32,64); every lane of a
 // group receives the group's total. The summation order is fixed, so results
 // are bitwise reproducible run to run.
@@ -111,8 +132,14 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (N >= 4) v += dpp<kDppXor2>(v);
   if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
   if constexpr (N >= 16) v += dpp<kDppMirror>(v);
-  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (N >= 32) {
+    const LanePair p = pair16(v);
+    v = p.lo + p.hi;
+  }
+  if constexpr (N >= 64) {
+    const LanePair p = pair32(v);
+    v = p.lo + p.hi;
+  }
   return v;
 }
 
@@ -122,8 +149,14 @@ __device__ __forceinline__ float group_max(float v) {
   if constexpr (N >= 4) v = fmaxf(v, dpp<kDppXor2>(v));
   if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
   if constexpr (N >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
-  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
-  if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  if constexpr (N >= 32) {
+    const LanePair p = pair16(v);
+    v = fmaxf(p.lo, p.hi);
+  }
+  if constexpr (N >= 64) {
+    const LanePair p = pair32(v);
+    v = fmaxf(p.lo, p.hi);
+  }
   return v;
 }
 

@@ -97,7 +97,7 @@ __device__ __forceinline__ void head_norm_rope(const u32x4 xr, const u32x4 wr, c
   const bool lower = d0 < D / 2;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    const float p = __shfl_xor(nv[e], LPS / 2, kWave);
+    const float p = LPS == 16 ? xor8(nv[e]) : __shfl_xor(nv[e], LPS / 2, kWave);
     const float rh = lower ? -p : p;
     out[e] = bf16r(bf16r(nv[e] * cs[e]) + bf16r(rh * sn[e]));
   }
