@@ -94,6 +94,10 @@ __device__ __forceinline__ void attn_begin(AttnPipe<LPR, U>& pp, const T* __rest
   const int tid = threadIdx.x;
   const int d0 = (tid % Geo::LPS) * Geo::EPL;
   attn_issue<Geo>(pp, kbase + d0, k_sn, vbase + d0, v_sn, start + tid / Geo::LPS, end);
+  // Keep the caller's query arithmetic below the loads: left free, the scheduler
+  // interleaves it with the address arithmetic, and its wait for the query rows
+  // then holds the K/V loads back by one round trip.
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // Packed bf16 pairs of EPL fp32 values that are exact bf16 (queries, new keys).
