@@ -468,7 +468,8 @@ struct AttnStep {
 
 // Attention partials of one decode step: block (kv head, split). Every load
 // that does not depend on arithmetic is issued first (queries, new key and
-// value, norm weights, RoPE rows, the first K/V rows of the split); the query
+// value and norm weights, then, once the position is in, the RoPE rows and the
+// first K/V rows of the split); the query
 // and the new key are normalised and rotated while those are in flight. The
 // block whose split holds slot p folds the new token in from registers (it is
 // not read back from the cache) and stores it to slot p for later steps; no
@@ -484,14 +485,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
   const int split = blockIdx.y;
   const int Hq = a.Hkv * G;
 
-  int64_t pos = *a.position;
-  pos = pos < 0 ? 0 : (pos >= a.cap ? a.cap - 1 : pos);
-  const int64_t len = pos + 1;
-  int64_t start, end;
-  attn_split_range(len, a.nsplit, split, start, end);
-  const bool owner = start <= pos && pos < end;  // block-uniform
-  const int64_t end_cached = owner ? pos : end;   // slot p comes from registers
-
+  // The rows that do not depend on the position go out before it is read.
   u32x4 qr[G], qw, kw, kr, vr, cr, sr;
 #pragma unroll
   for (int g = 0; g < G; ++g) qr[g] = ld16(a.qkv + (int64_t)(hk * G + g) * D + d0);
@@ -499,6 +493,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
   kw = ld16(a.k_norm_w + d0);
   kr = ld16(a.qkv + (int64_t)(Hq + hk) * D + d0);
   vr = ld16(a.qkv + (int64_t)(Hq + a.Hkv + hk) * D + d0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The position comes through the scalar cache: an earlier launch wrote it and
+  // nothing writes it during this one. The scalar load has its own wait counter,
+  // so waiting for it does not also wait for the rows above.
+  int64_t pos = *(const __attribute__((address_space(4))) int64_t*)a.position;
+  pos = pos < 0 ? 0 : (pos >= a.cap ? a.cap - 1 : pos);
+  const int64_t len = pos + 1;
+  int64_t start, end;
+  attn_split_range(len, a.nsplit, split, start, end);
+  const bool owner = start <= pos && pos < end;  // block-uniform
+  const int64_t end_cached = owner ? pos : end;   // slot p comes from registers
+
   cr = ld16(a.cos_t + pos * D + d0);
   sr = ld16(a.sin_t + pos * D + d0);
 
