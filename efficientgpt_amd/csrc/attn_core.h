@@ -196,9 +196,9 @@ __device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float
 // One block's partial softmax state over slots [start, end) of one kv head, for
 // the G query heads of its group (qf: this thread's EPL elements of each query,
 // in fp32), continuing from attn_begin(). If xk is non-null, one more slot with
-// key xk / value xv (this thread's EPL elements, fp32) is folded in by the
-// first stream of the block: the new token of a decode step, taken from
-// registers instead of being read back from the cache. Writes (m, l, acc[D])
+// key xk / value xv (this thread's EPL elements, fp32) starts the first stream
+// of the block: the new token of a decode step, taken from registers instead of
+// being read back from the cache. Writes (m, l, acc[D])
 // of every query head to
 //   ws_m[row + g * nsplit], ws_l[...], ws_acc[(row + g * nsplit) * D + d]
 // where row = (b * Hq + hk * G) * nsplit + split. An empty range with no extra
@@ -244,6 +244,38 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
   }
 
+  // The extra slot starts stream 0 (block-uniform branch): its score and value
+  // are in registers, so this runs while the first K/V rows are in flight and
+  // the stream continues from the state (m, l, acc) = (s, 1, v).
+  if (xk) {
+    uint32_t xkp[EPL / 2];
+    float xkf[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) xkf[e] = xk[e];
+    pack_bf16<EPL>(xkf, xkp);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float p = 0.f;
+      if constexpr (kAttnDot2<T>) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int i = 0; i < EPL / 2; ++i)
+          p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, xkp[i]),
+                                              __builtin_bit_cast(bf16x2_t, qp[g][i]), p, false);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], xk[e], p);
+      }
+      const float sx = group_sum<LPS>(p) * scale;
+      if (grp == 0) {
+        m[g] = sx;
+        l[g] = 1.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = xv[e];
+      }
+    }
+  }
+
   constexpr int64_t kStep = (int64_t)NG * U;  // slots one stream advances per iteration
   // Iterations are block-uniform: stream grp handles slots start + grp + i * NG.
   // Two register buffers (pp = A, pb = B) in pairs of iterations: the loads of
@@ -273,38 +305,6 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
     attn_mac<Geo, T, G>(pb, qf, qp, n0 + (it + 1) * kStep, end, scale, m, l, acc);
   } else if (it < nit) {
     attn_mac<Geo, T, G>(pp, qf, qp, n0 + it * kStep, end, scale, m, l, acc);
-  }
-
-  if (xk) {  // block-uniform: the extra slot goes to stream 0
-    uint32_t xkp[EPL / 2];
-    float xkf[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) xkf[e] = xk[e];
-    pack_bf16<EPL>(xkf, xkp);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float p = 0.f;
-      if constexpr (kAttnDot2<T>) {
-        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-#pragma unroll
-        for (int i = 0; i < EPL / 2; ++i)
-          p = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, xkp[i]),
-                                              __builtin_bit_cast(bf16x2_t, qp[g][i]), p, false);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) p = fmaf(qf[g][e], xk[e], p);
-      }
-      const float sx = group_sum<LPS>(p) * scale;
-      if (grp == 0) {
-        const float mt = fmaxf(m[g], sx);
-        const float alpha = exp2f((m[g] - mt) * kLog2e);  // 0 when the stream was empty
-        const float px = exp2f((sx - mt) * kLog2e);
-        l[g] = l[g] * alpha + px;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(px, xv[e], acc[g][e] * alpha);
-        m[g] = mt;
-      }
-    }
   }
 
   // Merge the groups of each wavefront: butterflies across groups (lane
