@@ -14,8 +14,7 @@
 // slot (16 lanes for bf16 with D = 128), so a wavefront reads 64 / LPS
 // consecutive slots (1 KiB) per load. Each LPS-lane group runs its own online
 // softmax over every NG-th slot of the split (NG = 256 / LPS groups); the
-// groups are merged by cross-lane butterflies within a wavefront, then the four
-// wavefronts through LDS.
+// streams are merged through LDS against the block's largest running max.
 #pragma once
 
 #include "common.h"
@@ -195,10 +194,12 @@ __device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float
 
 // One block's partial softmax state over slots [start, end) of one kv head, for
 // the G query heads of its group (qf: this thread's EPL elements of each query,
-// in fp32), continuing from attn_begin(). If xk is non-null, one more slot with
-// key xk / value xv (this thread's EPL elements, fp32) starts the first stream
-// of the block: the new token of a decode step, taken from registers instead of
-// being read back from the cache. Writes (m, l, acc[D])
+// in fp32), continuing from attn_begin(). If xnew is set (block-uniform), one
+// more slot with key xk / value xv (this thread's EPL elements, fp32) starts the
+// first stream of the block: the new token of a decode step, taken from
+// registers instead of being read back from the cache. The caller passes its
+// arrays whatever xnew is: selecting between them and a null pointer would make
+// the compiler keep them in scratch memory. Writes (m, l, acc[D])
 // of every query head to
 //   ws_m[row + g * nsplit], ws_l[...], ws_acc[(row + g * nsplit) * D + d]
 // where row = (b * Hq + hk * G) * nsplit + split. An empty range with no extra
@@ -216,7 +217,7 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
                                              int64_t v_sn, int64_t start, int64_t end, float scale,
                                              float* __restrict__ ws_m, float* __restrict__ ws_l,
                                              float* __restrict__ ws_acc, int64_t row, int nsplit,
-                                             const float* xk = nullptr, const float* xv = nullptr,
+                                             bool xnew = false, const float* xk = nullptr, const float* xv = nullptr,
                                              T* __restrict__ out = nullptr, int64_t o_sh = 0,
                                              uint32_t* __restrict__ tout = nullptr, uint32_t ttag = 0) {
   constexpr int EPL = Geo::EPL;
@@ -247,7 +248,7 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
   // The extra slot starts stream 0 (block-uniform branch): its score and value
   // are in registers, so this runs while the first K/V rows are in flight and
   // the stream continues from the state (m, l, acc) = (s, 1, v).
-  if (xk) {
+  if (xnew) {
     uint32_t xkp[EPL / 2];
     float xkf[EPL];
 #pragma unroll
@@ -307,69 +308,59 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
     attn_mac<Geo, T, G>(pp, qf, qp, n0 + it * kStep, end, scale, m, l, acc);
   }
 
-  // Merge the groups of each wavefront: butterflies across groups (lane
-  // distance LPS, 2*LPS, ...). Both partners end with the same merged state: at
-  // distances 16 and 32 each value arrives as the (lower, upper) partner pair
-  // (pair16 / pair32) and both lanes combine them in that order.
-#pragma unroll
-  for (int off = LPS; off < kWave; off *= 2) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      auto pair = [&](float v) -> LanePair {
-        if (off == 16) return pair16(v);
-        if (off == 32) return pair32(v);
-        const float o = __shfl_xor(v, off, kWave);
-        const bool upper = (threadIdx.x & off) != 0;
-        return upper ? LanePair{o, v} : LanePair{v, o};
-      };
-      const LanePair mp = pair(m[g]);
-      const LanePair lp = pair(l[g]);
-      const float mx = fmaxf(mp.lo, mp.hi);
-      const float wl = mx == -INFINITY ? 0.f : exp2f((mp.lo - mx) * kLog2e);
-      const float wh = mx == -INFINITY ? 0.f : exp2f((mp.hi - mx) * kLog2e);
-      l[g] = lp.lo * wl + lp.hi * wh;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const LanePair ap = pair(acc[g][e]);
-        acc[g][e] = ap.lo * wl + ap.hi * wh;
-      }
-      m[g] = mx;
-    }
-  }
-
-  // Merge the wavefronts through LDS and write this split's partial state.
+  // Merge the block's NG streams against the block maximum M of their m: M
+  // first (across the groups of a wavefront by lane exchanges, then across the
+  // wavefronts through LDS), then every stream scales its state by
+  // exp(m_s - M), one exponential per stream and query head, and the NG scaled
+  // states are summed through LDS in a fixed order (reproducible results).
   constexpr int kWaves = NT / kWave;
-  __shared__ float sm_m[kWaves][G];
-  __shared__ float sm_l[kWaves][G];
-  __shared__ float sm_acc[kWaves][G][D];
   const int wave = tid / kWave;
   const int lane = tid % kWave;
-  if (lane < LPS) {
+  __shared__ float sm_max[kWaves][G];
+  __shared__ float sm_l[NG][G];
+  __shared__ float sm_acc[NG][G][D];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g) {
+    float v = m[g];  // uniform over the LPS lanes of a stream
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) sm_acc[wave][g][d0 + e] = acc[g][e];
-      if (lane == 0) {
-        sm_m[wave][g] = m[g];
-        sm_l[wave][g] = l[g];
+    for (int off = LPS; off < kWave; off *= 2) {
+      if (off == 8) {
+        v = fmaxf(v, xor8(v));
+      } else if (off == 16) {
+        const LanePair p = pair16(v);
+        v = fmaxf(p.lo, p.hi);
+      } else if (off == 32) {
+        const LanePair p = pair32(v);
+        v = fmaxf(p.lo, p.hi);
+      } else {
+        v = fmaxf(v, __shfl_xor(v, off, kWave));
       }
     }
+    if (lane == 0) sm_max[wave][g] = v;
   }
-  __syncthreads();
+  lds_barrier();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mb = sm_max[0][g];
+#pragma unroll
+    for (int j = 1; j < kWaves; ++j) mb = fmaxf(mb, sm_max[j][g]);
+    const float w = m[g] == -INFINITY ? 0.f : exp2f((m[g] - mb) * kLog2e);  // 0 for an empty stream
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) sm_acc[grp][g][d0 + e] = acc[g][e] * w;
+    if (tid % LPS == 0) sm_l[grp][g] = l[g] * w;
+  }
+  lds_barrier();
   for (int i = tid; i < G * D; i += NT) {
     const int g = i / D;
     const int d = i % D;
-    float mx = -INFINITY;
+    float mx = sm_max[0][g];
 #pragma unroll
-    for (int j = 0; j < kWaves; ++j) mx = fmaxf(mx, sm_m[j][g]);
+    for (int j = 1; j < kWaves; ++j) mx = fmaxf(mx, sm_max[j][g]);
     float a = 0.f, ls = 0.f;
-    if (mx != -INFINITY) {
 #pragma unroll
-      for (int j = 0; j < kWaves; ++j) {
-        const float wj = exp2f((sm_m[j][g] - mx) * kLog2e);
-        a = fmaf(wj, sm_acc[j][g][d], a);
-        ls = fmaf(wj, sm_l[j][g], ls);
-      }
+    for (int j = 0; j < NG; ++j) {
+      a += sm_acc[j][g][d];
+      ls += sm_l[j][g];
     }
     if (out) {
       Elem<T>::store1(out + (int64_t)g * o_sh + d, a / ls);

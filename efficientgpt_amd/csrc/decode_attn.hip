@@ -61,7 +61,7 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(
   // One split: the block writes the output rows of its G query heads (no combine launch).
   T* o = nsplit == 1 ? out + (int64_t)b * o_sb + (int64_t)(hk * G) * o_sh : nullptr;
   attn_partial<Geo, T, G>(qf, pp, kb, k_sn, vb, v_sn, start, end, scale, ws_m, ws_l, ws_acc,
-                          ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit, nullptr, nullptr, o, o_sh);
+                          ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit, false, nullptr, nullptr, o, o_sh);
 }
 
 // Partial-softmax reduce: one block of kCombineThreads per (b, query head).

@@ -533,7 +533,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
 
   attn_partial<Geo, __bf16, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
                              a.scale, a.ws_m, a.ws_l, a.ws_acc, (int64_t)(hk * G) * a.nsplit + split, a.nsplit,
-                             owner ? kn : nullptr, owner ? vn : nullptr);
+                             owner, kn, vn);
 }
 
 // Merge of the split partials: one block per query head.

@@ -430,7 +430,7 @@ __device__ __forceinline__ void attention_block(const PArgs& a, const PLayer& L,
     gstore((u32x4*)(vc + pos * D + d0), vr);
   }
   attn_partial<Geo, __bf16, G>(qf, pp, (const __bf16*)kc, D, (const __bf16*)vc, D, 0, pos, a.scale, nullptr, nullptr,
-                               nullptr, 0, 1, kn, vn, nullptr, D, a.attn + (int64_t)hk * G * D, tag_out);
+                               nullptr, 0, 1, true, kn, vn, nullptr, D, a.attn + (int64_t)hk * G * D, tag_out);
 }
 
 // ------------------------------------------------------------------ the step
