@@ -57,64 +57,76 @@ struct FusedGemv {
   int64_t resid_ld;
   float* part_v;           // Argmax: per-block maxima (value, first index)
   int* part_i;
-  const float* ws_m;       // kXMerge: split-K partials of K / head_dim heads
+  const float* ws_m;       // merge sources: split-K partials of K / head_dim heads
   const float* ws_l;
   const float* ws_acc;
   int nsplit;
   int head_dim;
 };
 
-// Activation source of a fused GEMV.
-enum { kXRow = 0, kXMerge = 1 };
+// Activation source of a fused GEMV: XSRC = kXRow reads a row; XSRC = 4, 8 or
+// 16 merges the attention partials of at most that many splits.
+enum { kXRow = 0 };
 
 // Largest split count the o_proj prologue merges itself: all of a thread's
-// partial loads are issued together, unrolled to this bound.
+// partial loads are issued together, unrolled to the launch's bound.
 constexpr int kMergeInGemvMaxSplits = 16;
+
+// Unroll bound of the merge for a split count: the smallest of 4, 8, 16 that
+// holds it, so the prologue issues no more loads than one spare split's worth
+// per four.
+constexpr int merge_bound(int nsplit) { return nsplit <= 4 ? 4 : nsplit <= 8 ? 8 : 16; }
 
 // Stage the activation row of a fused GEMV in LDS as bf16 (the value every
 // wavefront of the block multiplies), once per block:
 //   kXRow, NORM: h = bf16(w * bf16(x * rsqrt(mean x^2 + eps)))   (x from a row or table[token])
 //   kXRow:       h = x
-//   kXMerge:     h = bf16(sum_s w_s acc_s / sum_s w_s l_s), w_s = exp(m_s - max m),
+//   merge:       h = bf16(sum_s w_s acc_s / sum_s w_s l_s), w_s = exp(m_s - max m),
 //                the split-K merge over K / head_dim heads, splits in order
 // Each thread owns 8 consecutive elements per pass; elements from K up to the
 // end of the last 1 KiB chunk are stored as 0. The loads are issued by
 // stage_load() BEFORE the kernel's weight loads: vector loads retire in order,
 // so the activation can then be used without waiting for the weight stream.
-template <int NTHREADS, int NCH>
+template <int NTHREADS, int NCH, int XSRC>
 struct Staged {
   static constexpr int kPasses = (NCH * kFChunk + NTHREADS * 8 - 1) / (NTHREADS * 8);
+  static constexpr int kSplits = XSRC == kXRow ? 1 : XSRC;
   u32x4 xv[kPasses], nv[kPasses];
-  float mv[kMergeInGemvMaxSplits], lv[kMergeInGemvMaxSplits];
-  u32x4 lo[kMergeInGemvMaxSplits], hi[kMergeInGemvMaxSplits];
+  float mv[kSplits], lv[kSplits];
+  u32x4 lo[kSplits], hi[kSplits];
 };
 
 template <int NTHREADS, int NCH, bool NORM, int XSRC>
-__device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS, NCH>& st) {
+__device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS, NCH, XSRC>& st) {
   const int tid = threadIdx.x;
   const u32x4 z{0u, 0u, 0u, 0u};
-  if constexpr (XSRC == kXMerge) {
-    // one pass: K <= NTHREADS * 8 is checked on the host
+  if constexpr (XSRC != kXRow) {
+    // One pass: K <= NTHREADS * 8 is checked on the host. Threads past K load
+    // nothing (whole wavefronts when K is a multiple of 512). The loads carry no
+    // per-split condition: slots past the split count re-read the last split,
+    // and stage_finish() gives them weight 0 (masking here would put a wait for
+    // the partials ahead of the weight loads).
     const int k8 = tid * 8;
-    const bool in_k = k8 < a.K;
-    const int D = a.head_dim;
-    const int h = in_k ? k8 / D : 0;
-    const int d = in_k ? k8 % D : 0;
-    const float* mrow = a.ws_m + (int64_t)h * a.nsplit;
-    const float* lrow = a.ws_l + (int64_t)h * a.nsplit;
-    const float* arow = a.ws_acc + (int64_t)h * a.nsplit * D + d;
+    if (k8 < a.K) {
+      const int D = a.head_dim;
+      const int h = k8 / D;
+      const int d = k8 - h * D;
+      const float* mrow = a.ws_m + (int64_t)h * a.nsplit;
+      const float* lrow = a.ws_l + (int64_t)h * a.nsplit;
+      const float* arow = a.ws_acc + (int64_t)h * a.nsplit * D + d;
 #pragma unroll
-    for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) {
-      const bool in = in_k && sp < a.nsplit;
-      st.mv[sp] = in ? mrow[sp] : -INFINITY;
-      st.lv[sp] = in ? lrow[sp] : 0.f;
-      st.lo[sp] = in ? ld16(arow + (int64_t)sp * D) : z;
-      st.hi[sp] = in ? ld16(arow + (int64_t)sp * D + 4) : z;
+      for (int sp = 0; sp < XSRC; ++sp) {
+        if (sp >= a.nsplit) break;  // uniform
+        st.mv[sp] = gload(mrow + sp);
+        st.lv[sp] = gload(lrow + sp);
+        st.lo[sp] = ld16(arow + (int64_t)sp * D);
+        st.hi[sp] = ld16(arow + (int64_t)sp * D + 4);
+      }
     }
   } else {
     const uint16_t* xr = token_row(a.x, a.x_token, a.x_ld, a.x_rows);
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH, XSRC>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
       const bool in = k8 < a.K;
       st.xv[p] = in ? ld16(xr + k8) : z;
@@ -124,21 +136,22 @@ __device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS, 
 }
 
 template <int NTHREADS, int NCH, bool NORM, int XSRC>
-__device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NTHREADS, NCH>& st, uint16_t* hs) {
+__device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NTHREADS, NCH, XSRC>& st, uint16_t* hs) {
   const int tid = threadIdx.x;
-  if constexpr (XSRC == kXMerge) {
+  if constexpr (XSRC != kXRow) {
     const int k8 = tid * 8;
     if (k8 >= a.K) {
       if (k8 < NCH * kFChunk) *(u32x4*)(hs + k8) = u32x4{0u, 0u, 0u, 0u};
     } else {
       float mx = -INFINITY;
 #pragma unroll
-      for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) mx = fmaxf(mx, st.mv[sp]);
+      for (int sp = 0; sp < XSRC; ++sp) mx = fmaxf(mx, sp < a.nsplit ? st.mv[sp] : -INFINITY);
       float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       float ls = 0.f;
 #pragma unroll
-      for (int sp = 0; sp < kMergeInGemvMaxSplits; ++sp) {
-        if (st.mv[sp] == -INFINITY) continue;  // empty (or absent) split: weight 0
+      for (int sp = 0; sp < XSRC; ++sp) {
+        // past the split count, or an empty split: weight 0
+        if (sp >= a.nsplit || st.mv[sp] == -INFINITY) continue;  // empty (or absent) split: weight 0
         const float wgt = exp2f((st.mv[sp] - mx) * kLog2e);
         const float v8[8] = {__uint_as_float(st.lo[sp].x), __uint_as_float(st.lo[sp].y),
                              __uint_as_float(st.lo[sp].z), __uint_as_float(st.lo[sp].w),
@@ -158,7 +171,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
     __shared__ float red[NTHREADS / kWave];
     float ss = 0.f;
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH, XSRC>::kPasses; ++p) {
       float v[8];
       Elem<__bf16>::unpack(st.xv[p], v);
 #pragma unroll
@@ -172,7 +185,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
     for (int j = 0; j < NTHREADS / kWave; ++j) total += red[j];
     const float inv = rsqrtf(total / (float)a.K + a.eps);
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH, XSRC>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
       if (k8 < NCH * kFChunk) {  // past K, x and w load as 0 and h is 0
         float v[8], w[8];
@@ -188,7 +201,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
     }
   } else {
 #pragma unroll
-    for (int p = 0; p < Staged<NTHREADS, NCH>::kPasses; ++p) {
+    for (int p = 0; p < Staged<NTHREADS, NCH, XSRC>::kPasses; ++p) {
       const int k8 = (p * NTHREADS + tid) * 8;
       if (k8 < NCH * kFChunk) *(u32x4*)(hs + k8) = st.xv[p];  // 0 past K
     }
@@ -339,7 +352,7 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
   int64_t t = (int64_t)blockIdx.x * W + wave;
 
   // Activation loads first (they retire first), then the weight stream.
-  Staged<W * kWave, NCH> stg;
+  Staged<W * kWave, NCH, XSRC> stg;
   stage_load<W * kWave, NCH, NORM, XSRC>(a, stg);
   const int8_t* rows[R];
   tile_rows<R, EPI>(a, t, rows);
@@ -727,7 +740,12 @@ int run_fused(const egpt_gemv_fused& p, hipStream_t st) {
     case EGPT_EPI_RESIDUAL:
       if (!p.y || !p.resid) return EGPT_ERR_INVALID;
       if (norm) return EGPT_ERR_UNSUPPORTED;
-      return merge ? launch_fused<kEpiResid, false, kXMerge>(a, st) : launch_fused<kEpiResid, false>(a, st);
+      if (!merge) return launch_fused<kEpiResid, false>(a, st);
+      switch (merge_bound(a.nsplit)) {
+        case 4: return launch_fused<kEpiResid, false, 4>(a, st);
+        case 8: return launch_fused<kEpiResid, false, 8>(a, st);
+        default: return launch_fused<kEpiResid, false, 16>(a, st);
+      }
     case EGPT_EPI_SWIGLU:
       if (!p.y) return EGPT_ERR_INVALID;
       if (!norm || merge) return EGPT_ERR_UNSUPPORTED;
