@@ -58,6 +58,12 @@ struct AttnGeom {
 template <typename T>
 constexpr bool kAttnDot2 = __is_same(T, __bf16);  // q . k on packed bf16 pairs
 
+// 2^x for softmax weights (x <= 0): the hardware v_exp_f32 alone. exp2f adds a
+// range reduction (compare, select, add, ldexp) only so that results below
+// 2^-126 come out as denormals instead of 0; a weight that small is below the
+// fp32 resolution of the sums it joins (each holds a term of weight 1).
+__device__ __forceinline__ float exp2_softmax(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // K/V rows in flight for one softmax stream: U slots, LPR 16-byte loads each.
 template <int LPR, int U>
 struct AttnPipe {
@@ -171,13 +177,15 @@ __device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float
     float mt = m[g];
 #pragma unroll
     for (int u = 0; u < U; ++u) mt = fmaxf(mt, s[u][g]);
-    if (mt == -INFINITY) continue;  // no valid slot yet in this stream
-    const float alpha = exp2f((m[g] - mt) * kLog2e);
+    // No valid slot yet in this stream (mt = -inf): exponents from 0 instead
+    // give alpha = 0 and p = 0, so the state stays (-inf, 0, 0) with no branch.
+    const float mref = mt == -INFINITY ? 0.f : mt;
+    const float alpha = exp2_softmax((m[g] - mref) * kLog2e);
     float p[U];
     float psum = 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      p[u] = exp2f((s[u][g] - mt) * kLog2e);  // 0 for invalid slots
+      p[u] = exp2_softmax((s[u][g] - mref) * kLog2e);  // 0 for invalid slots
       psum += p[u];
     }
     l[g] = l[g] * alpha + psum;
