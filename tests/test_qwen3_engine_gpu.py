@@ -20,6 +20,10 @@ pytestmark = pytest.mark.gpu
 SMALL = Qwen3Shape(vocab=2048, hidden=512, inter=1024, layers=3, heads=16, kv_heads=8, head_dim=128)
 # Qwen3-1.7B widths (hidden 2048, intermediate 6144, vocab 151936) at two layers
 WIDE2 = Qwen3Shape(vocab=151936, hidden=2048, inter=6144, layers=2, heads=16, kv_heads=8, head_dim=128)
+# Qwen3-8B head geometry (32 q / 8 kv heads: 4 query heads per kv head, o_proj over 4096 inputs) at a small width
+SMALL8 = Qwen3Shape(vocab=2048, hidden=512, inter=1024, layers=3, heads=32, kv_heads=8, head_dim=128)
+# Qwen3-8B widths (hidden 4096, intermediate 12288, 32 / 8 heads) at two layers and a short vocabulary
+WIDE8 = Qwen3Shape(vocab=4096, hidden=4096, inter=12288, layers=2, heads=32, kv_heads=8, head_dim=128)
 
 
 def build(shape, seed, std, cap):
@@ -99,11 +103,12 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
     assert agree / total >= 0.95, agree / total
 
 
-@pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048), (TINY, 0.2, 4096)])
+@pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048), (TINY, 0.2, 4096),
+                                           (SMALL8, 0.15, 96), (SMALL8, 0.15, 2048)])
 def test_fused_step_matches_unfused_step(shape, std, cap):
     """The fused step against the one-kernel-per-op step on the same tokens. cap 96 merges the
     attention splits inside the o_proj GEMV; cap 2048 (32 splits) and TINY at cap 4096 (2 kv heads, 64 splits)
-    take the separate merge launch."""
+    take the separate merge launch. SMALL8 runs 4 query heads per kv head, as Qwen3-8B does."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(3))
     runs = {}
@@ -151,6 +156,30 @@ def test_qwen3_1p7b_widths_match_oracle():
     got = eng.logits[0].float().cpu()
     want = logits.float()
     assert float((got - want).abs().max()) <= 2e-2 * float(want.abs().max())
+
+
+def test_qwen3_8b_widths_match_oracle():
+    """Qwen3-8B widths (hidden 4096, inter 12288, 32 / 8 heads) at two layers: teacher-forced greedy steps of the
+    fused step against the CPU oracle, and the last step's logits, at a cache past the o_proj merge bound (32
+    splits: the separate merge launch) and below it."""
+    for cap in (64, 2048):
+        eng, orc = build(WIDE8, seed=23, std=0.03, cap=cap)
+        prompt = torch.randint(0, WIDE8.vocab, (11,), generator=torch.Generator().manual_seed(6))
+        ref, margins, tops = oracle_greedy_with_margins(orc, prompt, 8)
+        assert len(set(ref)) > 3
+        a, n, bad = teacher_forced_agreement(eng, prompt, ref, margins, tops)
+        assert not bad, (cap, bad)
+        assert a >= n - 1, (cap, a, n)
+        orc.reset()
+        logits, pos = orc.forward(prompt, 0), len(prompt)
+        for t in ref[:-1]:
+            logits = orc.forward([t], pos)
+            pos += 1
+        got = eng.logits[0].float().cpu()
+        want = logits.float()
+        assert float((got - want).abs().max()) <= 2e-2 * float(want.abs().max()), cap
+        del eng, orc
+        torch.cuda.empty_cache()
 
 
 def test_graph_replay_equals_eager_step():
