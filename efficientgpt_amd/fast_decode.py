@@ -13,13 +13,45 @@ token, and run-ahead tokens past it are never emitted.
 over by an engine; int8 linears as they are, float linears quantised per output
 channel). The device step is the engine's captured graph: embedding through argmax
 and the token / position update, with no host synchronisation.
+
+Capacity buckets (assistant/backends.py:162-167, 221-249): `pick_bucket`,
+`GRAPH_BUCKETS` and `MAX_GRAPH_DECODERS` keep the reference's names and rule (the
+smallest bucket at or under the limit that holds prompt + new tokens, then the
+limit itself), and `DecoderPool` keeps one graph decoder per bucket in use, the
+least recently used dropped first. Here the buckets share one set of weight tensors
+(`Qwen3Int8Engine.with_capacity`); only caches, state and graphs are per bucket.
+Graph decoders built one per bucket from the same transformers model, as the
+reference's HFBackend does, share them too (`engine_for`).
 """
 
 import time
+import weakref
 
 import torch
 
 from .qwen3 import Qwen3Int8Engine
+
+# Engines taken over from a transformers model, per model: the first one owns the weight tensors, and
+# decoders of other capacities get engines sharing them (Qwen3Int8Engine.with_capacity). An engine
+# lives while a decoder holds it; the weight owner lives as long as the model.
+_MODEL_ENGINES = weakref.WeakKeyDictionary()  # model -> (weight owner, {capacity: engine, weakly held})
+
+
+def engine_for(model, max_cache_len):
+    """The engine of `max_cache_len` slots over a transformers model's weights, sharing them with every other
+    engine built from the same model."""
+    entry = _MODEL_ENGINES.get(model)
+    if entry is None:
+        owner = Qwen3Int8Engine.from_hf(model, max_cache_len)
+        entry = (owner, weakref.WeakValueDictionary())
+        entry[1][owner.cap] = owner
+        _MODEL_ENGINES[model] = entry
+    owner, by_cap = entry
+    eng = by_cap.get(int(max_cache_len))
+    if eng is None:
+        eng = owner.with_capacity(max_cache_len)
+        by_cap[eng.cap] = eng
+    return eng
 
 
 class GraphGreedyDecoder:
@@ -29,7 +61,7 @@ class GraphGreedyDecoder:
                 raise ValueError('engine cache is smaller than max_cache_len')
             self.engine = model
         else:
-            self.engine = Qwen3Int8Engine.from_hf(model, max_cache_len)
+            self.engine = engine_for(model, max_cache_len)
         self.model = model
         self.max_cache_len, self.lookahead = int(max_cache_len), int(lookahead)
         self.device = self.engine.device
@@ -90,3 +122,76 @@ class GraphGreedyDecoder:
         torch.cuda.synchronize(self.device)
         total = time.perf_counter() - t0
         return out, {'ttft_s': first - t0, 'total_s': total, 'tokens': len(out), 'capture_s': capture_s}
+
+
+# The reference's graph capacity buckets and pool size (assistant/backends.py:221-222).
+GRAPH_BUCKETS = (256, 384, 512, 1024, 2048, 4096)
+MAX_GRAPH_DECODERS = 3
+
+
+def pick_bucket(need, buckets, limit):
+    """Smallest cache capacity >= need among the buckets at or under `limit`, then `limit` itself; None if the
+    request does not fit (assistant/backends.py:162-167)."""
+    for c in sorted(b for b in buckets if b <= limit) + [limit]:
+        if c >= need:
+            return c
+    return None
+
+
+class DecoderPool:
+    """Graph decoders over one model, one per capacity bucket in use (assistant/backends.py:232-249).
+
+    `generate(input_ids, max_new_tokens, ...)` runs the request on the decoder of the smallest bucket that holds
+    prompt + max_new_tokens, capturing its graph on first use; at most `max_decoders` are kept, the least recently
+    used dropped first. Every bucket's engine shares the weight tensors of the first one. Stats are the
+    decoder's, plus `capacity` (the bucket) and `capture_s` including a new decoder's construction.
+    """
+
+    def __init__(self, model, limit=GRAPH_BUCKETS[-1], buckets=GRAPH_BUCKETS, max_decoders=MAX_GRAPH_DECODERS,
+                 lookahead=8):
+        if limit < 1:
+            raise ValueError('limit must be >= 1')
+        if max_decoders < 1:
+            raise ValueError('max_decoders must be >= 1')
+        self.model, self.limit, self.buckets = model, int(limit), tuple(int(b) for b in buckets)
+        self.max_decoders, self.lookahead = int(max_decoders), int(lookahead)
+        self.base = model if isinstance(model, Qwen3Int8Engine) else None  # a transformers model: engine_for()
+        self.decoders = {}  # capacity -> GraphGreedyDecoder, least recently used first
+
+    def capacity_for(self, need):
+        cap = pick_bucket(need, self.buckets, self.limit)
+        if cap is None:
+            raise ValueError('No capacity bucket large enough for request')
+        return cap
+
+    def decoder(self, need):
+        """The decoder for a request of `need` cache slots (built on first use) and its construction time."""
+        cap = self.capacity_for(need)
+        build_s = 0.0
+        if cap not in self.decoders:
+            while len(self.decoders) >= self.max_decoders:
+                del self.decoders[next(iter(self.decoders))]
+                torch.cuda.empty_cache()
+            t = time.perf_counter()
+            if self.base is None:
+                engine = engine_for(self.model, cap)
+            elif self.base.cap == cap and not any(d.engine is self.base for d in self.decoders.values()):
+                engine = self.base
+            else:
+                engine = self.base.with_capacity(cap)
+            self.decoders[cap] = GraphGreedyDecoder(engine, cap, lookahead=self.lookahead)
+            build_s = time.perf_counter() - t
+        dec = self.decoders.pop(cap)
+        self.decoders[cap] = dec  # most recently used
+        return dec, build_s
+
+    def generate(self, input_ids, max_new_tokens, eos_ids=(), on_token=None):
+        if input_ids.dim() != 2 or input_ids.shape[0] != 1:
+            raise ValueError('DecoderPool supports batch size 1')
+        if max_new_tokens < 1:
+            raise ValueError('max_new_tokens must be >= 1')
+        dec, build_s = self.decoder(input_ids.shape[1] + max_new_tokens)
+        out, st = dec.generate(input_ids, max_new_tokens, eos_ids=eos_ids, on_token=on_token)
+        st['capture_s'] = build_s + st.get('capture_s', 0.0)
+        st['capacity'] = dec.max_cache_len
+        return out, st

@@ -157,12 +157,11 @@ class Qwen3Int8Engine:
     def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False, persistent=None):
         if max_cache_len < 1:
             raise ValueError('max_cache_len must be >= 1')
-        self.cfg, self.cap = cfg, int(max_cache_len)
+        self.cfg = cfg
         self.device = torch.device(device)
         dev, bf = self.device, torch.bfloat16
         c = cfg
-        d = c.head_dim
-        self.n_qkv = (c.heads + 2 * c.kv_heads) * d
+        self.n_qkv = (c.heads + 2 * c.kv_heads) * c.head_dim
 
         def put(t, dtype=None):
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
@@ -174,11 +173,19 @@ class Qwen3Int8Engine:
         self.head_q, self.head_s = put(pk['head_q']), put(pk['head_s'], torch.float32)
         self.inv_freq = None if inv_freq is None else inv_freq.detach().float().cpu()
         del pk
-        cos, sin = rope_tables(c, self.cap, inv_freq)
-        self.cos, self.sin = put(cos), put(sin)
+        self._init_state(int(max_cache_len), persistent)
+
+    def _init_state(self, cap, persistent):
+        """Everything that depends on the cache capacity: RoPE tables, the K/V cache, the token / position state,
+        activation rows, workspaces and the fused step's descriptor. The weights are not touched."""
+        c, dev, bf = self.cfg, self.device, torch.bfloat16
+        d = c.head_dim
+        self.cap = cap
+        cos, sin = rope_tables(c, cap, self.inv_freq)
+        self.cos, self.sin = cos.to(dev).contiguous(), sin.to(dev).contiguous()
 
         # static state and activations
-        self.k_cache = torch.zeros(c.layers, c.kv_heads, self.cap, d, device=dev, dtype=bf)
+        self.k_cache = torch.zeros(c.layers, c.kv_heads, cap, d, device=dev, dtype=bf)
         self.v_cache = torch.zeros_like(self.k_cache)
         self.token = torch.zeros(1, dtype=torch.long, device=dev)
         self.position = torch.zeros(1, dtype=torch.long, device=dev)
@@ -193,16 +200,30 @@ class Qwen3Int8Engine:
         self.down = torch.zeros(1, c.hidden, device=dev, dtype=bf)
         self.logits = torch.zeros(1, c.vocab, device=dev, dtype=bf)
         lib = _lib.lib()
-        self.nsplit = lib.egpt_decode_attn_default_splits(1, c.kv_heads, self.cap)
+        self.nsplit = lib.egpt_decode_attn_default_splits(1, c.kv_heads, cap)
         need = ctypes.c_size_t()
         _lib.check('egpt_decode_attn_workspace',
-                   lib.egpt_decode_attn_workspace(1, c.heads, c.kv_heads, self.cap, d, self.nsplit, need))
+                   lib.egpt_decode_attn_workspace(1, c.heads, c.kv_heads, cap, d, self.nsplit, need))
         self.attn_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
         _lib.check('egpt_argmax_workspace', lib.egpt_argmax_workspace(c.vocab, need))
         self.arg_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
         self._build_step_desc()
         self.persistent = self._choose_persistent(persistent)
         self.graph = None
+
+    def with_capacity(self, max_cache_len, persistent=None):
+        """An engine over the same weight tensors (shared, not copied) with its own cache of max_cache_len slots,
+        its own state and its own graph: one per capacity bucket of a decoder pool."""
+        if max_cache_len < 1:
+            raise ValueError('max_cache_len must be >= 1')
+        other = object.__new__(type(self))
+        other.cfg, other.device, other.n_qkv = self.cfg, self.device, self.n_qkv
+        other.layers, other.embed, other.norm_w = self.layers, self.embed, self.norm_w
+        other.head_q, other.head_s, other.inv_freq = self.head_q, self.head_s, self.inv_freq
+        if hasattr(self, 'weights'):
+            other.weights = self.weights
+        other._init_state(int(max_cache_len), persistent)
+        return other
 
     def _choose_persistent(self, want):
         """Whether step() is the one-launch persistent step (egpt_qwen3_persistent_step).

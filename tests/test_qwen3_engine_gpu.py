@@ -217,6 +217,30 @@ def test_eos_stops_exactly_and_never_leaks_lookahead_tokens():
     assert again == full
 
 
+def test_decoder_pool_buckets_share_weights_and_match_a_single_decoder():
+    """DecoderPool (the reference's capacity buckets, assistant/backends.py:232-249): each request runs on the
+    smallest bucket that holds it, every bucket's engine shares the weight tensors, the least recently used decoder
+    is dropped past max_decoders, and the tokens equal a plain graph decoder's at the same capacity."""
+    from efficientgpt_amd.fast_decode import DecoderPool, GraphGreedyDecoder
+    eng, _ = build(TINY, seed=9, std=0.2, cap=128)
+    pool = DecoderPool(eng, limit=512, buckets=(64, 128, 256), max_decoders=2)
+    g = torch.Generator().manual_seed(11)
+    requests = [(5, 20, 64), (37, 60, 128), (5, 200, 256), (9, 30, 64), (37, 60, 128)]
+    for p, n, cap in requests:
+        x = torch.randint(0, TINY.vocab, (1, p), generator=g).cuda()
+        got, st = pool.generate(x, n)
+        assert st['capacity'] == cap and st['tokens'] == n and len(got) == n
+        dec = pool.decoders[cap]
+        assert dec.engine.layers is eng.layers and dec.engine.head_q is eng.head_q
+        assert dec.engine.cap == cap
+        assert len(pool.decoders) <= 2
+        want, _ = GraphGreedyDecoder(eng.with_capacity(cap), cap).generate(x, n)  # an engine of its own
+        assert got == want, (p, n, cap)
+    assert list(pool.decoders) == [64, 128]  # 256 was the least recently used when 128 came back
+    with pytest.raises(ValueError):
+        pool.generate(torch.zeros((1, 400), dtype=torch.long, device='cuda'), 200)
+
+
 def test_guards():
     from efficientgpt_amd.fast_decode import GraphGreedyDecoder
     eng, _ = build(TINY, seed=0, std=0.2, cap=32)
@@ -254,6 +278,14 @@ def test_transformers_model_int8_through_graph_decoder():
         ref, margins, tops = oracle_greedy_with_margins(orc, x[0], 40)
         ok, where = near_tie_match(ref, got, margins, tops)
         assert ok, (p, where)
+    # a decoder of another capacity over the same model (the reference's HFBackend builds one per bucket) shares
+    # the weight tensors and decodes the same tokens at the same capacity's arithmetic
+    dec256 = GraphGreedyDecoder(model, max_cache_len=256)
+    assert dec256.engine.layers is dec.engine.layers and dec256.engine.cap == 256
+    assert GraphGreedyDecoder(model, max_cache_len=128).engine is dec.engine
+    again, _ = dec256.generate(x.cuda(), 40)
+    ok, where = near_tie_match(ref, again, margins, tops)
+    assert ok, where
 
 
 def test_hf_attention_adapter_matches_oracle_attention():
