@@ -34,6 +34,7 @@ Prints one JSON line:
 
 import argparse
 import ctypes
+import itertools
 import json
 import math
 import os
@@ -62,6 +63,9 @@ def parse():
     ap.add_argument('--no-extra', action='store_true', help='skip the attention and copy measurements')
     ap.add_argument('--step', choices=('fused', 'persistent'), default='fused',
                     help='decode step form: five launches per layer (default) or one persistent launch per token')
+    ap.add_argument('--dispatch-grid', action='store_true',
+                    help='instead of the decode benchmark: single-pass against default split-K decode attention over '
+                         'batch x heads x cache length (one JSON line per point), the data behind the split policy')
     return ap.parse_args()
 
 
@@ -355,12 +359,38 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
             'token_agreement_with_gpu': agree}
 
 
+def dispatch_grid(inner=20, reps=20):
+    """Single pass (1 split) against the default split count of egpt_decode_attn, bf16, every row at position
+    cap - 1, 20 calls per captured graph (warm: the point is the launch structure, not HBM). MHA 6 x 64 (the
+    reference's Phase-5 shape), and 16 / 8 and 32 / 8 heads at D 128 (Qwen3-1.7B / -8B)."""
+    from efficientgpt_amd.decode_attention import decode_attention, decode_attention_single_pass
+    for (hq, hkv, d), b, cap in itertools.product([(6, 6, 64), (16, 8, 128), (32, 8, 128)],
+                                                   [1, 2, 4, 8, 16, 32, 64, 128], [16, 32, 64, 128, 256, 1024, 4096]):
+        q = torch.randn(b, hq, 1, d, device='cuda', dtype=torch.bfloat16)
+        k = torch.randn(b, hkv, cap, d, device='cuda', dtype=torch.bfloat16)
+        v = torch.randn_like(k)
+        pos = torch.full((b,), cap - 1, device='cuda', dtype=torch.long)
+
+        def many(fn):
+            return lambda: [fn() for _ in range(inner)]
+        t1 = min(_time_graph(many(lambda: decode_attention_single_pass(q, k, v, pos)), reps) for _ in range(3))
+        ts = min(_time_graph(many(lambda: decode_attention(q, k, v, pos)), reps) for _ in range(3))
+        print(json.dumps({'hq': hq, 'hkv': hkv, 'd': d, 'batch': b, 'cap': cap,
+                          'single_pass_us': round(t1 / inner * 1e6, 2), 'default_us': round(ts / inner * 1e6, 2)}),
+              flush=True)
+        del q, k, v
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({'error': 'this build measures one GPU; runs on several GPUs are not part of it',
                           'n_gpus': args.gpus}), flush=True)
         sys.exit(2)
+    if args.dispatch_grid:
+        torch.cuda.set_device(0)
+        dispatch_grid()
+        return
     from efficientgpt_amd.fast_decode import GraphGreedyDecoder
     from efficientgpt_amd.qwen3 import QWEN3_1_7B, QWEN3_8B, Qwen3Int8Engine
 

@@ -883,6 +883,19 @@ extern "C" int egpt_argmax_parts(const float* part_v, const int* part_i, int par
   return EGPT_LAUNCH_STATUS();
 }
 
+extern "C" int egpt_qwen3_step_default_splits(int kv_heads, int cap) {
+  if (kv_heads < 1 || cap < 1) return 1;
+  // About one block per CU and at least 64 slots per split. No one-pass floor
+  // for short caches: the step merges the splits without a launch of their own
+  // up to kMergeInGemvMaxSplits.
+  const int by_len = (cap + 63) / 64;
+  int by_grid = (256 + kv_heads - 1) / kv_heads;
+  if (by_grid < 1) by_grid = 1;
+  int n = by_len < by_grid ? by_len : by_grid;
+  if (n > 256) n = 256;
+  return n < 1 ? 1 : n;
+}
+
 extern "C" int egpt_qwen3_step_workspace(const egpt_qwen3_step* s, size_t* bytes) {
   if (!s || !bytes || s->heads < 1 || s->kv_heads < 1 || s->nsplit < 1 || s->head_dim < 1 || s->vocab < 1)
     return EGPT_ERR_INVALID;

@@ -113,9 +113,13 @@ def decode_attention_single_pass(q, k, v, position, block_n=64, warps=2):
 
 # Shape-only dispatch (positions live on the device inside a graph): single pass when
 # there are enough (row, kv head) programs to fill the GPU or the cache is short.
-# Mirrors research/phase5/decode_attention.py:157-169; thresholds are this kernel's.
-SINGLE_PASS_MIN_PROGRAMS = 512
-SINGLE_PASS_MAX_CAPACITY_FEW_PROGRAMS = 32
+# Mirrors research/phase5/decode_attention.py:157-169; the thresholds are this
+# kernel's, from its dispatch grid on the MI355X (`bench.py --dispatch-grid`): up to
+# 256 slots one pass is 1.0-1.8x faster, and from 256 programs on both forms time
+# the same. They are where egpt_decode_attn_default_splits returns 1, so
+# decode_attention() with no config makes the same choice.
+SINGLE_PASS_MIN_PROGRAMS = 256
+SINGLE_PASS_MAX_CAPACITY_FEW_PROGRAMS = 256
 
 
 def use_single_pass(batch, heads, capacity):

@@ -94,6 +94,8 @@ int egpt_int8_gemm(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, con
  * (research/phase5/decode_attention.py:22-71, :74-103); nsplit 1 is the
  * single-pass kernel (:106-151): one launch, which writes out directly.
  */
+/* The default split count: 1 up to 256 slots (no combine launch), then about one
+ * block per CU, at least 64 slots per split, at most 256 splits. */
 int egpt_decode_attn_default_splits(int B, int Hkv, int cap);
 int egpt_decode_attn_workspace(int B, int Hq, int Hkv, int cap, int D, int nsplit, size_t *bytes);
 int egpt_decode_attn(int dtype,
@@ -276,6 +278,12 @@ typedef struct egpt_qwen3_step {
 } egpt_qwen3_step;
 
 int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
+/* The step's split count for `nsplit`: about one block per CU and at least 64
+ * slots per split, at any cache length. Unlike the stand-alone attention, the
+ * step merges the splits in the o_proj GEMV's prologue (up to 16) or in one small
+ * launch, so short caches split too (5-8 splits beat 1-4 at 400 slots, 16 q / 8
+ * kv heads). Has no counterpart in the reference, whose step reads SDPA. */
+int egpt_qwen3_step_default_splits(int kv_heads, int cap);
 int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
 
 /*

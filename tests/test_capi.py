@@ -57,6 +57,23 @@ def test_default_splits_bounded(b, hkv, cap):
     assert 1 <= n <= 256 and n <= max(1, cap)
 
 
+def test_split_policies():
+    """The stand-alone attention runs one pass up to 256 slots and wherever 256 (row, kv head) programs fill the
+    GPU; past that about one block per CU with at least 64 slots per split. The decode step splits short caches
+    too (its merge needs no launch of its own). Host functions: no GPU is touched."""
+    from efficientgpt_amd.decode_attention import use_single_pass
+    lib = _lib.lib()
+    for b, hkv in ((1, 8), (4, 6), (16, 8), (32, 8), (64, 6)):
+        for cap in (1, 2, 63, 64, 65, 128, 255, 256, 257, 400, 1024, 4096, 32768, 131072):
+            n = lib.egpt_decode_attn_default_splits(b, hkv, cap)
+            assert (n == 1) == use_single_pass(b, hkv, cap), (b, hkv, cap, n)
+            if cap > 256:
+                assert n == min(-(-cap // 64), -(-256 // (b * hkv)), 256), (b, hkv, cap, n)
+    assert [lib.egpt_qwen3_step_default_splits(8, c) for c in (64, 96, 256, 400, 2048, 32768)] == [1, 2, 4, 7, 32, 32]
+    assert lib.egpt_qwen3_step_default_splits(2, 4096) == 64
+    assert lib.egpt_qwen3_step_default_splits(0, 100) == 1
+
+
 def test_struct_layouts_match_the_header(tmp_path):
     """The ctypes mirrors of egpt_gemv_fused / egpt_qwen3_step / egpt_qwen3_layer have the C layout."""
     import shutil
