@@ -73,8 +73,7 @@ enum { kXRow = 0 };
 constexpr int kMergeInGemvMaxSplits = 16;
 
 // Unroll bound of the merge for a split count: the smallest of 4, 8, 16 that
-// holds it, so the prologue issues no more loads than one spare split's worth
-// per four.
+// holds it, so the unrolled prologue is not much longer than the launch needs.
 constexpr int merge_bound(int nsplit) { return nsplit <= 4 ? 4 : nsplit <= 8 ? 8 : 16; }
 
 // Stage the activation row of a fused GEMV in LDS as bf16 (the value every
@@ -102,10 +101,11 @@ __device__ __forceinline__ void stage_load(const FusedGemv& a, Staged<NTHREADS, 
   const u32x4 z{0u, 0u, 0u, 0u};
   if constexpr (XSRC != kXRow) {
     // One pass: K <= NTHREADS * 8 is checked on the host. Threads past K load
-    // nothing (whole wavefronts when K is a multiple of 512). The loads carry no
-    // per-split condition: slots past the split count re-read the last split,
-    // and stage_finish() gives them weight 0 (masking here would put a wait for
-    // the partials ahead of the weight loads).
+    // nothing (whole wavefronts when K is a multiple of 512). The loop stops at
+    // the split count with a wave-uniform (scalar) branch; slots past it are
+    // neither loaded nor masked here, since a select on the loaded values would
+    // put a wait for the partials ahead of the weight loads: stage_finish()
+    // gives them weight 0.
     const int k8 = tid * 8;
     if (k8 < a.K) {
       const int D = a.head_dim;
@@ -150,8 +150,7 @@ __device__ __forceinline__ void stage_finish(const FusedGemv& a, const Staged<NT
       float ls = 0.f;
 #pragma unroll
       for (int sp = 0; sp < XSRC; ++sp) {
-        // past the split count, or an empty split: weight 0
-        if (sp >= a.nsplit || st.mv[sp] == -INFINITY) continue;  // empty (or absent) split: weight 0
+        if (sp >= a.nsplit || st.mv[sp] == -INFINITY) continue;  // past the split count, or empty: weight 0
         const float wgt = exp2f((st.mv[sp] - mx) * kLog2e);
         const float v8[8] = {__uint_as_float(st.lo[sp].x), __uint_as_float(st.lo[sp].y),
                              __uint_as_float(st.lo[sp].z), __uint_as_float(st.lo[sp].w),
@@ -482,11 +481,11 @@ struct AttnStep {
 // Attention partials of one decode step: block (kv head, split). Every load
 // that does not depend on arithmetic is issued first (queries, new key and
 // value and norm weights, then, once the position is in, the RoPE rows and the
-// first K/V rows of the split); the query
-// and the new key are normalised and rotated while those are in flight. The
-// block whose split holds slot p folds the new token in from registers (it is
-// not read back from the cache) and stores it to slot p for later steps; no
-// other block of the launch touches slot p, so no barrier orders the store.
+// first K/V rows of the split); the query and the new key are normalised and
+// rotated while those are in flight. The block whose split holds slot p starts
+// its first softmax stream with the new token from registers (it is not read
+// back from the cache) and stores it to slot p for later steps; no other block
+// of the launch touches slot p, so no barrier orders the store.
 template <int D, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep a) {
   using Geo = AttnGeom<__bf16, D, kAttnThreads, 1, 4>;
