@@ -207,8 +207,8 @@ __device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float
 // first stream of the block: the new token of a decode step, taken from
 // registers instead of being read back from the cache. The caller passes its
 // arrays whatever xnew is: selecting between them and a null pointer would make
-// the compiler keep them in scratch memory. Writes (m, l, acc[D])
-// of every query head to
+// the compiler keep them in scratch memory. Writes (m, l, acc[D]) of every query
+// head to
 //   ws_m[row + g * nsplit], ws_l[...], ws_acc[(row + g * nsplit) * D + d]
 // where row = (b * Hq + hk * G) * nsplit + split. An empty range with no extra
 // slot gives the empty state (m = -inf, l = 0, acc = 0). With `out` set (one
