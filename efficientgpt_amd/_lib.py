@@ -33,7 +33,7 @@ SIGNATURES = {
     'egpt_int8_gemv_splitk': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
                                        _c_int, _c_vp, _c_size, _c_vp]),
     'egpt_decode_attn_default_splits': (_c_int, [_c_int, _c_int, _c_int]),
-    'egpt_qwen3_step_default_splits': (_c_int, [_c_int, _c_int]),
+    'egpt_qwen3_step_default_splits': (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     'egpt_decode_attn_workspace': (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
     'egpt_decode_attn': (_c_int, [_c_int,
                                   _c_vp, _c_i64, _c_i64,

@@ -200,7 +200,7 @@ class Qwen3Int8Engine:
         self.down = torch.zeros(1, c.hidden, device=dev, dtype=bf)
         self.logits = torch.zeros(1, c.vocab, device=dev, dtype=bf)
         lib = _lib.lib()
-        self.nsplit = lib.egpt_qwen3_step_default_splits(c.kv_heads, cap)
+        self.nsplit = lib.egpt_qwen3_step_default_splits(c.heads, c.kv_heads, d, cap)
         need = ctypes.c_size_t()
         _lib.check('egpt_decode_attn_workspace',
                    lib.egpt_decode_attn_workspace(1, c.heads, c.kv_heads, cap, d, self.nsplit, need))

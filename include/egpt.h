@@ -282,8 +282,10 @@ int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
  * slots per split, at any cache length. Unlike the stand-alone attention, the
  * step merges the splits in the o_proj GEMV's prologue (up to 16) or in one small
  * launch, so short caches split too (5-8 splits beat 1-4 at 400 slots, 16 q / 8
- * kv heads). Has no counterpart in the reference, whose step reads SDPA. */
-int egpt_qwen3_step_default_splits(int kv_heads, int cap);
+ * kv heads); up to 2048 slots, with an o_proj row (heads * head_dim) of at most
+ * 2048, it stays at 16 splits so that the prologue merges them. Has no
+ * counterpart in the reference, whose step reads SDPA. */
+int egpt_qwen3_step_default_splits(int heads, int kv_heads, int head_dim, int cap);
 int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
 
 /*

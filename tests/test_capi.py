@@ -69,9 +69,14 @@ def test_split_policies():
             assert (n == 1) == use_single_pass(b, hkv, cap), (b, hkv, cap, n)
             if cap > 256:
                 assert n == min(-(-cap // 64), -(-256 // (b * hkv)), 256), (b, hkv, cap, n)
-    assert [lib.egpt_qwen3_step_default_splits(8, c) for c in (64, 96, 256, 400, 2048, 32768)] == [1, 2, 4, 7, 32, 32]
-    assert lib.egpt_qwen3_step_default_splits(2, 4096) == 64
-    assert lib.egpt_qwen3_step_default_splits(0, 100) == 1
+    step = lib.egpt_qwen3_step_default_splits
+    # Qwen3-1.7B geometry (16 / 8 heads, D 128): the 16-split cap up to 2048 slots
+    assert [step(16, 8, 128, c) for c in (64, 96, 256, 400, 1024, 1025, 1772, 2048, 2049, 32768)] == \
+        [1, 2, 4, 7, 16, 16, 16, 16, 32, 32]
+    # Qwen3-8B geometry (32 / 8 heads): a 4096-wide o_proj keeps more splits
+    assert [step(32, 8, 128, c) for c in (400, 1772, 2048, 8192)] == [7, 28, 32, 32]
+    assert step(4, 2, 32, 4096) == 64
+    assert step(0, 8, 128, 100) == 1 and step(16, 0, 128, 100) == 1
 
 
 def test_struct_layouts_match_the_header(tmp_path):

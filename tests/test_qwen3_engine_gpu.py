@@ -106,9 +106,10 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
 @pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048), (TINY, 0.2, 4096),
                                            (SMALL8, 0.15, 96), (SMALL8, 0.15, 2048)])
 def test_fused_step_matches_unfused_step(shape, std, cap):
-    """The fused step against the one-kernel-per-op step on the same tokens. cap 96 merges the
-    attention splits inside the o_proj GEMV; cap 2048 (32 splits) and TINY at cap 4096 (2 kv heads, 64 splits)
-    take the separate merge launch. SMALL8 runs 4 query heads per kv head, as Qwen3-8B does."""
+    """The fused step against the one-kernel-per-op step on the same tokens. cap 96, and SMALL at cap 2048 (16
+    splits), merge the attention splits inside the o_proj GEMV; SMALL8 at cap 2048 (32 splits: a 4096-wide o_proj)
+    and TINY at cap 4096 (2 kv heads, 64 splits) take the separate merge launch. SMALL8 runs 4 query heads per kv
+    head, as Qwen3-8B does."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(3))
     runs = {}
