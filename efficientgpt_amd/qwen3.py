@@ -23,8 +23,9 @@ Step (token t at position p; writes K/V slot p, attends to slots 0..p):
   embed -> [add+]RMSNorm -> QKV GEMV -> q/k norm + RoPE + cache write -> split-K
   attention + combine -> o GEMV -> add+RMSNorm -> gate_up GEMV -> SiLU*up ->
   down GEMV -> ... -> add+final RMSNorm -> lm_head GEMV -> argmax (token, p + 1).
-Prefill runs the same kernels over all prompt rows (linears past 16 rows take the
-reference's dequantised GEMM formula, int8_linear.py:96-97), outside the graph.
+Prefill runs the same kernels over all prompt rows, outside the graph; linears past 16
+rows take the reference's prefill formula (int8_linear.py:96-97) on the MFMA GEMM that
+reads the int8 weights, and on the library GEMM past its row limit.
 """
 
 import ctypes

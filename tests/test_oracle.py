@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP kernels."""
+"""Pins the CPU oracle (oracle/) before the HIP kernels are tested against it."""
 
 import numpy as np
 import pytest
