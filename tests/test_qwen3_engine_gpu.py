@@ -183,6 +183,29 @@ def test_qwen3_8b_widths_match_oracle():
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL, 2048), (SMALL8, 2048)])
+def test_fused_step_ignores_cache_past_position(shape, cap):
+    """NaN in every cache slot past the position leaves the fused step's logits bit-identical: the reference's
+    poisoning test of its split kernel (research/phase5/test_graph_gpu.py:250-261) run on the whole step, through
+    the o_proj merge (2 and 16 splits) and the separate merge launch (32 splits)."""
+    eng, _ = build(shape, seed=13, std=0.15, cap=cap)
+    prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(4))
+    runs = []
+    for fill in (0.0, float('nan')):
+        eng.reset()
+        eng.prefill(prompt)
+        eng.k_cache[:, :, len(prompt):] = fill
+        eng.v_cache[:, :, len(prompt):] = fill
+        logits = []
+        for _ in range(6):
+            eng.step()
+            logits.append(eng.logits[0].clone())
+        torch.cuda.synchronize()
+        runs.append(logits)
+    assert all(torch.equal(a, b) for a, b in zip(*runs))
+    assert not any(bool(torch.isnan(a.float()).any()) for a in runs[0])
+
+
 def test_graph_replay_equals_eager_step():
     eng, _ = build(SMALL, seed=5, std=0.05, cap=64)
     prompt = torch.arange(7) * 13
