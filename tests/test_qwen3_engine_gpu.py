@@ -183,11 +183,12 @@ def test_qwen3_8b_widths_match_oracle():
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL, 2048), (SMALL8, 2048)])
+@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL8, 96), (SMALL, 2048), (SMALL8, 2048)])
 def test_fused_step_ignores_cache_past_position(shape, cap):
     """NaN in every cache slot past the position leaves the fused step's logits bit-identical: the reference's
     poisoning test of its split kernel (research/phase5/test_graph_gpu.py:250-261) run on the whole step, through
-    the o_proj merge (2 and 16 splits) and the separate merge launch (32 splits)."""
+    the o_proj merge (2 and 16 splits) and the separate merge launch (32 splits), with attention blocks of one query
+    head (cap 96) and of a kv head's whole group (cap 2048)."""
     eng, _ = build(shape, seed=13, std=0.15, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(4))
     runs = []
