@@ -492,10 +492,11 @@ struct AttnStep {
 // holds at most this many slots, and a whole kv head's group of query heads
 // (reading its K/V once) past it. Short caches are latency-bound: a block with
 // one head finishes its loop and its merge sooner, and reading each K/V row once
-// per query head costs little. Measured on the MI355X with 128-token prompts:
-// Qwen3-1.7B (2 query heads per kv head) 2.5-3% faster, Qwen3-8B (4) 5.7%; at
-// 3.3k-3.8k slots both 4.5-5% slower.
-constexpr int kHeadBlockMaxSlots = 1024;
+// per query head costs little. Measured on the MI355X, with the split counts of
+// egpt_qwen3_step_default_splits, against whole-group blocks: Qwen3-1.7B (2
+// query heads per kv head) 4.9% faster at 392 slots and 4.5-5.4% at 1264-1764,
+// Qwen3-8B (4) 5.7% and 2.6-3.3%; at 3.3k-3.8k slots both 4.5-5% slower.
+constexpr int kHeadBlockMaxSlots = 2048;
 
 // Attention partials of one decode step: block (query heads hq0 .. hq0 + G - 1
 // of one kv head, split). Every load that does not depend on arithmetic is
@@ -909,26 +910,19 @@ extern "C" int egpt_qwen3_step_default_splits(int heads, int kv_heads, int head_
   const int by_len = (cap + 63) / 64;
   // Attention blocks of one query head (kHeadBlockMaxSlots): at most 4 splits up
   // to 512 slots and 8 past that, so the o_proj prologue merges them at its
-  // 4- or 8-split bound. Measured on the MI355X against the rule below (7, 11
-  // and 16 splits at 392, 664 and 964 slots): Qwen3-1.7B 1.9%, 5.8% and 3%
-  // faster, Qwen3-8B 1.7% and 6% at 392 and 964 slots.
+  // 4- or 8-split bound. Measured on the MI355X against about one block per CU
+  // (7, 11, 16 and 16 splits at 392, 664, 964 and 1764 slots): Qwen3-1.7B 1.9%,
+  // 5.8%, 3% and 4.5% faster, Qwen3-8B 1.7%, 6% and 3.3% at 392, 964 and 1764.
   if (cap <= kHeadBlockMaxSlots) {
     const int lim = cap <= 512 ? 4 : 8;
     return by_len < lim ? by_len : lim;
   }
-  // About one block per CU and at least 64 slots per split. No one-pass floor
-  // for short caches: the step merges the splits without a launch of their own
-  // up to kMergeInGemvMaxSplits.
+  // Past that, about one block per CU and at least 64 slots per split (more than
+  // kMergeInGemvMaxSplits are merged by a launch of their own).
   int by_grid = (256 + kv_heads - 1) / kv_heads;
   if (by_grid < 1) by_grid = 1;
   int n = by_len < by_grid ? by_len : by_grid;
   if (n > 256) n = 256;
-  // Up to 2048 slots, and when the o_proj row is at most 2048 wide (the merge
-  // then runs on at most 256 threads of its block), 16 splits merged in the
-  // prologue beat more splits plus the merge launch: Qwen3-1.7B at 1772 slots
-  // 1312 against 1277 tok/s with 28 splits. Longer caches, and Qwen3-8B's
-  // 4096-wide o_proj, keep the rule above.
-  if (n > kMergeInGemvMaxSplits && cap <= 2048 && heads * head_dim <= 2048) n = kMergeInGemvMaxSplits;
   return n < 1 ? 1 : n;
 }
 

@@ -104,12 +104,12 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
 
 
 @pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048), (TINY, 0.2, 4096),
-                                           (SMALL8, 0.15, 96), (SMALL8, 0.15, 2048)])
+                                           (SMALL8, 0.15, 96), (SMALL8, 0.15, 4096)])
 def test_fused_step_matches_unfused_step(shape, std, cap):
-    """The fused step against the one-kernel-per-op step on the same tokens. cap 96, and SMALL at cap 2048 (16
-    splits), merge the attention splits inside the o_proj GEMV; SMALL8 at cap 2048 (32 splits: a 4096-wide o_proj)
-    and TINY at cap 4096 (2 kv heads, 64 splits) take the separate merge launch. SMALL8 runs 4 query heads per kv
-    head, as Qwen3-8B does."""
+    """The fused step against the one-kernel-per-op step on the same tokens. Up to 2048 slots the attention blocks
+    serve one query head and the o_proj GEMV merges their 2 or 8 splits; at 4096 slots (32 splits, TINY 64) the blocks
+    serve a kv head's whole group and a launch of its own merges the splits. SMALL8 runs 4 query heads per kv head,
+    as Qwen3-8B does."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(3))
     runs = {}
@@ -161,9 +161,10 @@ def test_qwen3_1p7b_widths_match_oracle():
 
 def test_qwen3_8b_widths_match_oracle():
     """Qwen3-8B widths (hidden 4096, inter 12288, 32 / 8 heads) at two layers: teacher-forced greedy steps of the
-    fused step against the CPU oracle, and the last step's logits, at a cache past the o_proj merge bound (32
-    splits: the separate merge launch) and below it."""
-    for cap in (64, 2048):
+    fused step against the CPU oracle, and the last step's logits, with attention blocks of one query head (64 slots,
+    splits merged in the o_proj GEMV) and of a kv head's whole group (4096 slots, 32 splits: the separate merge
+    launch)."""
+    for cap in (64, 4096):
         eng, orc = build(WIDE8, seed=23, std=0.03, cap=cap)
         prompt = torch.randint(0, WIDE8.vocab, (11,), generator=torch.Generator().manual_seed(6))
         ref, margins, tops = oracle_greedy_with_margins(orc, prompt, 8)
@@ -183,12 +184,12 @@ def test_qwen3_8b_widths_match_oracle():
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL8, 96), (SMALL, 2048), (SMALL8, 2048)])
+@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL8, 96), (SMALL, 2048), (SMALL8, 4096)])
 def test_fused_step_ignores_cache_past_position(shape, cap):
     """NaN in every cache slot past the position leaves the fused step's logits bit-identical: the reference's
     poisoning test of its split kernel (research/phase5/test_graph_gpu.py:250-261) run on the whole step, through
-    the o_proj merge (2 and 16 splits) and the separate merge launch (32 splits), with attention blocks of one query
-    head (cap 96) and of a kv head's whole group (cap 2048)."""
+    the o_proj merge (2 and 8 splits) with attention blocks of one query head, and the separate merge launch (32
+    splits) with blocks of a kv head's whole group."""
     eng, _ = build(shape, seed=13, std=0.15, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(4))
     runs = []
