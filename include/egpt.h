@@ -278,13 +278,14 @@ typedef struct egpt_qwen3_step {
 } egpt_qwen3_step;
 
 int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
-/* The step's split count for `nsplit`: about one block per CU and at least 64
- * slots per split, at any cache length. Unlike the stand-alone attention, the
- * step merges the splits in the o_proj GEMV's prologue (up to 16) or in one small
- * launch, so short caches split too (5-8 splits beat 1-4 at 400 slots, 16 q / 8
- * kv heads); up to 2048 slots, with an o_proj row (heads * head_dim) of at most
- * 2048, it stays at 16 splits so that the prologue merges them. Has no
- * counterpart in the reference, whose step reads SDPA. */
+/* The step's split count for `nsplit`. Up to 2048 slots, where the step's
+ * attention blocks serve one query head each: one split per 64 slots, at most 4
+ * up to 512 slots and 8 past that, merged in the o_proj GEMV's prologue. Past
+ * 2048 slots (blocks of a kv head's whole group): about one block per CU and at
+ * least 64 slots per split, merged in one small launch past 16. Unlike the
+ * stand-alone attention, the step splits short caches too, since its merge needs
+ * no launch of its own. Has no counterpart in the reference, whose step reads
+ * SDPA. */
 int egpt_qwen3_step_default_splits(int heads, int kv_heads, int head_dim, int cap);
 int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
 
