@@ -324,8 +324,7 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
     torch.set_num_threads(host_threads())
     shape = Qwen3Shape(c.vocab, c.hidden, c.inter, c.layers, c.heads, c.kv_heads, c.head_dim, c.rope_theta,
                        c.rms_eps, c.tied)
-    w = {k: v.cpu() for k, v in eng.weights.items()}
-    orc = Qwen3Oracle(shape, w, dtype=torch.bfloat16, cap=len(prompt) + n_tokens + 1)
+    orc = Qwen3Oracle(shape, eng.weights, dtype=torch.bfloat16, cap=len(prompt) + n_tokens + 1)
     margins = []  # (top-1 - top-2, top-1) of the oracle's logits at each step
 
     def pick(logits):
@@ -400,7 +399,9 @@ def main():
     n_stream = 256 if args.model == 'qwen3-1.7b' else 64
     cap = args.prompt + max(args.warmup + args.steps, n_stream) + 8
     t = time.perf_counter()
-    eng = Qwen3Int8Engine.random(cfg, cap, seed=args.seed, device=dev, persistent=args.step == 'persistent')
+    want_cpu = args.cpu_tokens > 0 and args.model == 'qwen3-1.7b'
+    eng = Qwen3Int8Engine.random(cfg, cap, seed=args.seed, device=dev, persistent=args.step == 'persistent',
+                                 keep_weights=want_cpu)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(args.seed + 1))

@@ -37,15 +37,40 @@ def hipcc():
     return str(path) if path.exists() else 'hipcc'
 
 
-def build(verbose=False):
-    """Compile csrc/*.hip into libegpt_hip.so (atomic replace). Raises on failure."""
-    tmp = LIB.with_suffix('.so.tmp')
-    cmd = [hipcc(), *HIPCC_FLAGS, *sources(), '-o', str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(' '.join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f'hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}')
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def build(verbose=False, jobs=None):
+    """Compile csrc/*.hip into libegpt_hip.so (atomic replace). Raises on failure.
+
+    Each source is compiled to its own object in parallel (the translation units share
+    no device symbols), then the objects are linked into the shared library."""
+    objdir = PKG / '_build'
+    objdir.mkdir(exist_ok=True)
+    jobs = jobs or min(16, os.cpu_count() or 1)
+    compile_flags = [f for f in HIPCC_FLAGS if f != '-shared']
+    pending = [(src, objdir / (Path(src).stem + '.o')) for src in sources()]
+    running, objects = [], []
+    while pending or running:
+        while pending and len(running) < jobs:
+            src, obj = pending.pop(0)
+            objects.append(obj)
+            running.append((src, _run([hipcc(), *compile_flags, '-c', src, '-o', str(obj)], verbose)))
+        src, proc = running.pop(0)
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            for _, other in running:
+                other.kill()
+            raise RuntimeError(f'hipcc failed on {src} ({proc.returncode}):\n{err[-4000:]}')
+    tmp = LIB.with_suffix('.so.tmp')
+    link = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, objects), '-o', str(tmp)]
+    proc = _run(link, verbose)
+    _, err = proc.communicate()
+    if proc.returncode != 0:
+        raise RuntimeError(f'hipcc link failed ({proc.returncode}):\n{err[-4000:]}')
     os.replace(tmp, LIB)
     return LIB
 

@@ -3,16 +3,20 @@
 Drop-in for research/realmodel/fast_decode.py: `GraphGreedyDecoder(model,
 max_cache_len, lookahead=8)` and `.generate(input_ids, max_new_tokens, eos_ids=(),
 on_token=None) -> (tokens, stats)` keep the reference's names, guards (ValueError),
-stats keys and host-loop semantics (:66-111): each step enqueues a non-blocking copy
-of its token into pinned host memory and records an event; the host emits every
-token whose event has completed, never blocking on the step it just launched; the
-run-ahead is bounded by `lookahead`, EOS stops emission at (and including) the EOS
-token, and run-ahead tokens past it are never emitted.
+stats keys and streaming semantics (:66-111): every step's token is copied into
+pinned host memory behind an event, a token is handed out as soon as its event has
+fired, the host never waits on the step it has just launched unless more than
+`lookahead` steps are in flight, EOS stops the run at (and including) the EOS token,
+and tokens that steps launched ahead of it computed are never handed out.
 
-`model` is a Qwen3Int8Engine or a transformers Qwen3 model (its weights are taken
-over by an engine; int8 linears as they are, float linears quantised per output
-channel). The device step is the engine's captured graph: embedding through argmax
-and the token / position update, with no host synchronisation.
+`model` is a Qwen3Int8Engine or a transformers Qwen3 model whose linears are int8
+(`quantize_model(model)`, which the reference's HFBackend runs for quant='int8'
+before it builds its decoder, assistant/backends.py:200-202, 241). A model with
+float linears is refused: the engine runs the int8 contract only, and quantising
+behind the caller's back would change the tokens the caller asked for.
+`quantize=True` opts in to that. The device step is the engine's captured graph:
+embedding through argmax and the token / position update, with no host
+synchronisation.
 
 Capacity buckets (assistant/backends.py:162-167, 221-249): `pick_bucket`,
 `GRAPH_BUCKETS` and `MAX_GRAPH_DECODERS` keep the reference's names and rule (the
@@ -24,6 +28,7 @@ Graph decoders built one per bucket from the same transformers model, as the
 reference's HFBackend does, share them too (`engine_for`).
 """
 
+import collections
 import time
 import weakref
 
@@ -37,12 +42,12 @@ from .qwen3 import Qwen3Int8Engine
 _MODEL_ENGINES = weakref.WeakKeyDictionary()  # model -> (weight owner, {capacity: engine, weakly held})
 
 
-def engine_for(model, max_cache_len):
-    """The engine of `max_cache_len` slots over a transformers model's weights, sharing them with every other
-    engine built from the same model."""
+def engine_for(model, max_cache_len, quantize=False):
+    """The engine of `max_cache_len` slots over a transformers model's int8 weights, sharing them with every
+    other engine built from the same model (see Qwen3Int8Engine.from_hf for `quantize`)."""
     entry = _MODEL_ENGINES.get(model)
     if entry is None:
-        owner = Qwen3Int8Engine.from_hf(model, max_cache_len)
+        owner = Qwen3Int8Engine.from_hf(model, max_cache_len, quantize=quantize)
         entry = (owner, weakref.WeakValueDictionary())
         entry[1][owner.cap] = owner
         _MODEL_ENGINES[model] = entry
@@ -55,13 +60,13 @@ def engine_for(model, max_cache_len):
 
 
 class GraphGreedyDecoder:
-    def __init__(self, model, max_cache_len, lookahead=8):
+    def __init__(self, model, max_cache_len, lookahead=8, quantize=False):
         if isinstance(model, Qwen3Int8Engine):
             if model.cap < max_cache_len:
                 raise ValueError('engine cache is smaller than max_cache_len')
             self.engine = model
         else:
-            self.engine = engine_for(model, max_cache_len)
+            self.engine = engine_for(model, max_cache_len, quantize=quantize)
         self.model = model
         self.max_cache_len, self.lookahead = int(max_cache_len), int(lookahead)
         self.device = self.engine.device
@@ -71,57 +76,60 @@ class GraphGreedyDecoder:
     def graph(self):
         return self.engine.graph
 
-    @torch.inference_mode()
-    def generate(self, input_ids, max_new_tokens, eos_ids=(), on_token=None):
+    def _check_request(self, input_ids, max_new_tokens):
         if input_ids.dim() != 2 or input_ids.shape[0] != 1:
             raise ValueError('GraphGreedyDecoder supports batch size 1')
-        p = input_ids.shape[1]
         if max_new_tokens < 1:
             raise ValueError('max_new_tokens must be >= 1')
-        if p < 1:
+        if input_ids.shape[1] < 1:
             raise ValueError('prompt must hold at least one token')
-        if p + max_new_tokens > self.max_cache_len:
+        if input_ids.shape[1] + max_new_tokens > self.max_cache_len:
             raise ValueError('prompt + max_new_tokens exceeds max_cache_len')
+
+    @torch.inference_mode()
+    def generate(self, input_ids, max_new_tokens, eos_ids=(), on_token=None):
+        self._check_request(input_ids, max_new_tokens)
         eng = self.engine
         capture_s = 0.0
-        if eng.graph is None:
+        if eng.graph is None:  # first request: capture the step (timed apart from TTFT)
             t = time.perf_counter()
             eng.capture()
-            capture_s = time.perf_counter() - t  # reported separately, not inside TTFT
+            capture_s = time.perf_counter() - t
         eng.reset()
-        eos = set(int(e) for e in eos_ids)
+        stop = frozenset(int(e) for e in eos_ids)
+        tokens, t_first = [], None
+        in_flight = collections.deque()  # (host slot, event after its copy), oldest first
         t0 = time.perf_counter()
-        eng.prefill(input_ids[0])  # leaves the first new token in eng.token, position = p
-        events, out, emitted, first, launched, done = [], [], 0, None, 0, False
-        while not done:
-            self.host[launched:launched + 1].copy_(eng.token, non_blocking=True)
-            ev = torch.cuda.Event()
-            ev.record()
-            events.append(ev)
-            launched += 1
-            if launched < max_new_tokens:
-                eng.graph.replay()  # computes the next token into eng.token
-            while emitted < launched and (events[emitted].query() or launched - emitted > self.lookahead
-                                          or launched >= max_new_tokens):
-                events[emitted].synchronize()
-                tok = int(self.host[emitted])
+        eng.prefill(input_ids[0])  # the first new token is now in eng.token
+        for step in range(max_new_tokens):
+            self.host[step:step + 1].copy_(eng.token, non_blocking=True)
+            copied = torch.cuda.Event()
+            copied.record()
+            in_flight.append((step, copied))
+            final = step + 1 == max_new_tokens
+            if not final:
+                eng.graph.replay()  # overwrites eng.token with the next step's pick
+            # hand out what has landed; block only to keep the run-ahead within the lookahead, or at the end
+            while in_flight and (final or len(in_flight) > self.lookahead or in_flight[0][1].query()):
+                slot, copied = in_flight.popleft()
+                copied.synchronize()
+                tok = int(self.host[slot])
                 if tok < 0:  # the persistent step's failure mark
                     eng.check_status()
                     raise RuntimeError('decode step reported a failure')
-                if first is None:
-                    first = time.perf_counter()
-                out.append(tok)
+                if t_first is None:
+                    t_first = time.perf_counter()
+                tokens.append(tok)
                 if on_token:
                     on_token(tok)
-                emitted += 1
-                if tok in eos:
-                    done = True
+                if tok in stop:
+                    in_flight.clear()
                     break
-            if launched >= max_new_tokens and emitted >= launched:
-                done = True
+            if tokens and tokens[-1] in stop:
+                break
         torch.cuda.synchronize(self.device)
         total = time.perf_counter() - t0
-        return out, {'ttft_s': first - t0, 'total_s': total, 'tokens': len(out), 'capture_s': capture_s}
+        return tokens, {'ttft_s': t_first - t0, 'total_s': total, 'tokens': len(tokens), 'capture_s': capture_s}
 
 
 # The reference's graph capacity buckets and pool size (assistant/backends.py:221-222).
@@ -148,13 +156,14 @@ class DecoderPool:
     """
 
     def __init__(self, model, limit=GRAPH_BUCKETS[-1], buckets=GRAPH_BUCKETS, max_decoders=MAX_GRAPH_DECODERS,
-                 lookahead=8):
+                 lookahead=8, quantize=False):
         if limit < 1:
             raise ValueError('limit must be >= 1')
         if max_decoders < 1:
             raise ValueError('max_decoders must be >= 1')
         self.model, self.limit, self.buckets = model, int(limit), tuple(int(b) for b in buckets)
         self.max_decoders, self.lookahead = int(max_decoders), int(lookahead)
+        self.quantize = bool(quantize)
         self.base = model if isinstance(model, Qwen3Int8Engine) else None  # a transformers model: engine_for()
         self.decoders = {}  # capacity -> GraphGreedyDecoder, least recently used first
 
@@ -174,7 +183,7 @@ class DecoderPool:
                 torch.cuda.empty_cache()
             t = time.perf_counter()
             if self.base is None:
-                engine = engine_for(self.model, cap)
+                engine = engine_for(self.model, cap, quantize=self.quantize)
             elif self.base.cap == cap and not any(d.engine is self.base for d in self.decoders.values()):
                 engine = self.base
             else:

@@ -288,8 +288,11 @@ class Qwen3Int8Engine:
 
     @classmethod
     @torch.no_grad()
-    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda', persistent=None):
-        """Random-init weights N(0, std) (bf16, norms 1), quantised per output channel on the device."""
+    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda', persistent=None, keep_weights=False):
+        """Random-init weights N(0, std) (bf16, norms 1), quantised per output channel on the device.
+
+        keep_weights: also keep a HOST copy of the transformers-named int8 weights as `.weights` (what a CPU
+        model of the same network is built from); the device holds only the engine's packed layout."""
         dev = torch.device(device)
         g = torch.Generator(device=dev).manual_seed(seed)
 
@@ -319,15 +322,28 @@ class Qwen3Int8Engine:
         else:
             w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(w['model.embed_tokens.weight'])
         eng = cls(cfg, w, max_cache_len, device=dev, persistent=persistent)
-        eng.weights = w  # kept so a CPU oracle can be built from the very same tensors
+        if keep_weights:
+            eng.weights = {k: v.cpu() for k, v in w.items()}
+        del w
         return eng
 
     @classmethod
     @torch.no_grad()
-    def from_hf(cls, model, max_cache_len):
-        """Engine over a transformers Qwen3ForCausalLM (int8 linears taken as they are, float ones quantised)."""
+    def from_hf(cls, model, max_cache_len, quantize=False):
+        """Engine over a transformers Qwen3ForCausalLM whose linears (lm_head included) are int8, as
+        `quantize_model(model)` leaves them; their codes and scales are taken as they are.
+
+        A model with float linears is refused (ValueError) unless `quantize=True`: the engine runs every
+        linear on the int8 contract, so running such a model here would change its output. With
+        quantize=True the float linears are quantised per output channel (research/realmodel/int8_linear.py:
+        106-117) and a tied float head from the embedding."""
         cfg = Qwen3Config.from_hf(model.config)
         sd = dict(model.state_dict())
+        names = [f'model.layers.{i}.{n}' for i in range(cfg.layers) for n in LINEARS] + ['lm_head']
+        floats = [n for n in names if n + '.qweight' not in sd]
+        if floats and not quantize:
+            raise ValueError(f'{len(floats)} linear layers are not int8 (first: {floats[0]}); this decoder runs the '
+                             'int8 weight-only path: call quantize_model(model) first, or pass quantize=True')
         if 'lm_head.qweight' not in sd and cfg.tied:
             sd.pop('lm_head.weight', None)  # tied float head: quantise from the embedding
         device = next(model.parameters()).device

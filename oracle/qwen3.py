@@ -84,24 +84,48 @@ def rotate_half(x):
 
 
 class Linear:
-    """A float weight, or int8 codes + fp32 scales applied by the reference's row rule."""
+    """A float weight, or int8 codes + fp32 scales applied by the reference's row rule.
 
-    def __init__(self, weight=None, qweight=None, scale=None):
+    `ksplit` > 1 takes the decode formula's fp32 sum the way the reference's split-K
+    GEMV does (research/realmodel/int8_linear.py:41-64, :79-80): partial sums over
+    chunks of KCHUNK = ceil(ceil(K / ksplit) / 128) * 128 columns, added in chunk
+    order, then scaled and rounded once. It is the same product summed in another
+    valid fp32 order, which is what tests use it for: two forms of the reference's own
+    arithmetic whose difference measures how far rounding alone moves a result.
+    """
+
+    def __init__(self, weight=None, qweight=None, scale=None, ksplit=1):
         self.weight = weight
         self.q = qweight
         self.s = scale
+        self.ksplit = ksplit
         self._qf = None
 
-    def __call__(self, x):
+    def _sum(self, x):
+        """fp32 x @ q^T, in one product or by the split-K chunks."""
+        xf = x.float()
+        k = xf.shape[-1]
+        if self.ksplit <= 1:
+            return xf @ self._qf.t()
+        kchunk = -(-(-(-k // self.ksplit)) // 128) * 128
+        acc = None
+        for k0 in range(0, k, kchunk):
+            part = xf[..., k0:k0 + kchunk] @ self._qf[:, k0:k0 + kchunk].t()
+            acc = part if acc is None else acc + part
+        return acc
+
+    def __call__(self, x, rule=None):
+        """`rule` None picks by row count as the reference's op does (int8_linear.py:92-98); 'decode' applies
+        the decode kernel's per-row formula to every row (what that many single-row calls compute)."""
         if self.q is None:
             return x @ self.weight.t()
         if self._qf is None:
             self._qf = self.q.float()  # exact image of the codes, cached
-        acc = x.float() @ self._qf.t()
         if x.dtype != torch.bfloat16:
-            return (acc * self.s).to(x.dtype)
-        if x.reshape(-1, x.shape[-1]).shape[0] <= MAX_DECODE_ROWS:
-            return (acc * self.s).to(torch.bfloat16)
+            return (x.float() @ self._qf.t() * self.s).to(x.dtype)
+        if rule == 'decode' or (rule is None and x.reshape(-1, x.shape[-1]).shape[0] <= MAX_DECODE_ROWS):
+            return (self._sum(x) * self.s).to(torch.bfloat16)
+        acc = x.float() @ self._qf.t()  # prefill: the library GEMM, no split-K form
         return (acc.to(torch.bfloat16).float() * self.s).to(torch.bfloat16)
 
 
@@ -134,13 +158,23 @@ class Qwen3Oracle:
         self.cos, self.sin = rope_tables(shape, cap, dtype, inv_freq)
         self.reset()
 
+    def set_ksplit(self, ksplit):
+        """Sum every int8 linear's decode formula in `ksplit` chunks (Linear.ksplit); 1 is the one-pass form."""
+        for layer in self.layers:
+            for n in LINEARS:
+                layer[n].ksplit = ksplit
+        self.lm_head.ksplit = ksplit
+
     def reset(self):
         s = self.shape
         self.k_cache = [torch.zeros(s.kv_heads, self.cap, s.head_dim, dtype=self.dtype) for _ in range(s.layers)]
         self.v_cache = [torch.zeros(s.kv_heads, self.cap, s.head_dim, dtype=self.dtype) for _ in range(s.layers)]
 
-    def _attention(self, q, layer, pos0):
-        """q [T, Hq, D] at positions pos0..pos0+T-1 over cache slots 0..position: fp32 math."""
+    def _attention(self, q, layer, pos0, chunk=512):
+        """q [T, Hq, D] at positions pos0..pos0+T-1 over cache slots 0..position: fp32 math.
+
+        Query rows are taken `chunk` at a time (each row's result depends on that row alone), so a long prompt
+        never holds more than Hq x chunk x slots scores."""
         s = self.shape
         t = q.shape[0]
         g = s.heads // s.kv_heads
@@ -149,17 +183,27 @@ class Qwen3Oracle:
         v = self.v_cache[layer][:, :n].float()
         k = k.repeat_interleave(g, dim=0)  # [Hq, n, D]
         v = v.repeat_interleave(g, dim=0)
-        qf = q.float().transpose(0, 1)  # [Hq, T, D]
-        scores = (qf @ k.transpose(1, 2)) * (s.head_dim ** -0.5)
+        kt = k.transpose(1, 2)
         slots = torch.arange(n)
-        allowed = slots[None, :] <= (pos0 + torch.arange(t))[:, None]
-        scores = scores.masked_fill(~allowed[None], float('-inf'))
-        out = torch.softmax(scores, dim=-1) @ v  # [Hq, T, D]
-        return out.transpose(0, 1).reshape(t, s.heads * s.head_dim).to(self.dtype)
+        out = torch.empty(t, s.heads * s.head_dim, dtype=self.dtype)
+        for r0 in range(0, t, chunk):
+            r1 = min(t, r0 + chunk)
+            m = n - (t - r1)  # slots the last row of this chunk may see
+            qf = q[r0:r1].float().transpose(0, 1)  # [Hq, rows, D]
+            scores = (qf @ kt[:, :, :m]) * (s.head_dim ** -0.5)
+            allowed = slots[None, :m] <= (pos0 + torch.arange(r0, r1))[:, None]
+            scores = scores.masked_fill(~allowed[None], float('-inf'))
+            o = torch.softmax(scores, dim=-1) @ v[:, :m]  # [Hq, rows, D]
+            out[r0:r1] = o.transpose(0, 1).reshape(r1 - r0, s.heads * s.head_dim).to(self.dtype)
+        return out
 
     @torch.no_grad()
-    def forward(self, tokens, pos0):
-        """tokens: 1-D ids at positions pos0.. ; writes the cache; returns last-row logits [vocab]."""
+    def forward(self, tokens, pos0, all_logits=False, rule=None):
+        """tokens: 1-D ids at positions pos0.. ; writes the cache; returns last-row logits [vocab].
+
+        all_logits: return every row's logits [T, vocab] instead. rule='decode': every linear uses the decode
+        formula on every row, so T rows at once compute what T single-token decode steps would (each row sees
+        slots 0..its own position): the teacher-forced form of a greedy decode."""
         s = self.shape
         tokens = torch.as_tensor(tokens, dtype=torch.long).reshape(-1)
         t = tokens.numel()
@@ -170,9 +214,9 @@ class Qwen3Oracle:
         sin = self.sin[pos0:pos0 + t][:, None, :]
         for i, L in enumerate(self.layers):
             h = rms_norm(x, L['input_layernorm'], s.rms_eps)
-            q = L['self_attn.q_proj'](h).view(t, s.heads, s.head_dim)
-            k = L['self_attn.k_proj'](h).view(t, s.kv_heads, s.head_dim)
-            v = L['self_attn.v_proj'](h).view(t, s.kv_heads, s.head_dim)
+            q = L['self_attn.q_proj'](h, rule).view(t, s.heads, s.head_dim)
+            k = L['self_attn.k_proj'](h, rule).view(t, s.kv_heads, s.head_dim)
+            v = L['self_attn.v_proj'](h, rule).view(t, s.kv_heads, s.head_dim)
             q = rms_norm(q, L['self_attn.q_norm'], s.rms_eps)
             k = rms_norm(k, L['self_attn.k_norm'], s.rms_eps)
             q = (q * cos) + (rotate_half(q) * sin)
@@ -180,11 +224,14 @@ class Qwen3Oracle:
             self.k_cache[i][:, pos0:pos0 + t] = k.transpose(0, 1)
             self.v_cache[i][:, pos0:pos0 + t] = v.transpose(0, 1)
             a = self._attention(q, i, pos0)
-            x = x + L['self_attn.o_proj'](a)
+            x = x + L['self_attn.o_proj'](a, rule)
             h = rms_norm(x, L['post_attention_layernorm'], s.rms_eps)
-            x = x + L['mlp.down_proj'](F.silu(L['mlp.gate_proj'](h)) * L['mlp.up_proj'](h))
-        x = rms_norm(x, self.norm, s.rms_eps)
-        return self.lm_head(x[-1:])[0]
+            x = x + L['mlp.down_proj'](F.silu(L['mlp.gate_proj'](h, rule)) * L['mlp.up_proj'](h, rule), rule)
+        # the head always sees one row per call in a decode (logits_to_keep=1): the decode formula
+        if all_logits:
+            return self.lm_head(rms_norm(x, self.norm, s.rms_eps), 'decode')
+        x = rms_norm(x[-1:], self.norm, s.rms_eps)
+        return self.lm_head(x, 'decode')[0]
 
     def greedy(self, prompt, n_new, with_margins=False):
         """Greedy ids of n_new tokens after `prompt` (and each step's top-1 minus top-2 logit if asked)."""

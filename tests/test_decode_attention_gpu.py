@@ -41,15 +41,17 @@ def splitk_err(q, k, v, pos, truth):
     return float(np.abs(got.astype(np.float64) - truth).max())
 
 
-def run_case(b, hq, hkv, cap, d, dtype, pos, scale=1.0, seed=0, floor=None, config=None):
+def run_case(b, hq, hkv, cap, d, dtype, pos, scale=1.0, seed=0, floor=None, config=None, fn=None):
     from efficientgpt_amd.decode_attention import decode_attention
+    if fn is None:
+        fn = (lambda q, k, v, p: decode_attention(q, k, v, p, config=config))
     g = torch.Generator().manual_seed(seed)
     q = (torch.randn(b, hq, 1, d, generator=g) * scale).to(dtype)
     k = (torch.randn(b, hkv, cap, d, generator=g) * scale).to(dtype)
     v = torch.randn(b, hkv, cap, d, generator=g).to(dtype)
     pos = torch.as_tensor(pos, dtype=torch.long)
     truth = oatt.attention_truth(q.double().numpy(), k.double().numpy(), v.double().numpy(), pos.numpy())
-    out = decode_attention(q.cuda(), k.cuda(), v.cuda(), pos.cuda(), config=config)
+    out = fn(q.cuda(), k.cuda(), v.cuda(), pos.cuda())
     assert out.dtype == dtype and out.shape == (b, hq, 1, d)
     err = float(np.abs(out.double().cpu().numpy() - truth).max())
     if floor is None:
@@ -170,3 +172,31 @@ def test_graph_capture_follows_device_position():
         eager = decode_attention(q, k, v, torch.tensor([p], device='cuda'))
         torch.cuda.synchronize()
         assert torch.equal(out, eager), p
+
+
+@pytest.mark.parametrize('b,hq,hkv,cap', [
+    (32, 16, 8, 1024),   # 256 (row, kv head) programs: single pass
+    (31, 16, 8, 1024),   # 248 programs, 1024 slots: split-K
+    (1, 16, 8, 256),     # few programs, 256 slots: single pass
+    (1, 16, 8, 257),     # few programs, 257 slots: split-K
+    (16, 6, 6, 256),     # the reference's Phase-5 MHA shape at its cache size
+    (64, 6, 6, 1024),    # 384 programs: single pass
+])
+def test_dispatch_both_sides_of_its_thresholds(b, hq, hkv, cap):
+    """decode_attention_dispatch (research/phase5/decode_attention.py:157-169; its tests test_graph_gpu.py:400-405)
+    picks single pass exactly where use_single_pass says, and each choice meets the oracle's bounds. Its output
+    is bit-identical to the form it chose."""
+    from efficientgpt_amd.decode_attention import (decode_attention, decode_attention_dispatch,
+                                                   decode_attention_single_pass, use_single_pass)
+    d = 128 if hq != 6 else 64
+    pos = torch.randint(0, cap, (b,), generator=torch.Generator().manual_seed(b + cap))
+    pos[0] = cap - 1
+    out = run_case(b, hq, hkv, cap, d, torch.bfloat16, pos, seed=3, fn=decode_attention_dispatch)
+    single = use_single_pass(b, hkv, cap)
+    assert single == (b * hkv >= 256 or cap <= 256)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(b, hq, 1, d, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(b, hkv, cap, d, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(b, hkv, cap, d, generator=g).to(torch.bfloat16).cuda()
+    chosen = decode_attention_single_pass if single else decode_attention
+    assert torch.equal(out, chosen(q, k, v, pos.cuda()))

@@ -1,0 +1,229 @@
+"""The decode path at the two full-size model workloads, checked against the CPU oracle.
+
+Qwen3-1.7B: the whole 28-layer model (hidden 2048, intermediate 6144, 16 q / 8 kv heads
+of 128, vocab 151936, tied head), weights N(0, 0.02), a 128-token uniform-random
+prompt and 256 greedy tokens through GraphGreedyDecoder (one graph replay per token).
+The oracle (oracle/qwen3.py) runs teacher-forced on the decoder's own tokens: the
+prompt with the prefill rule, then all 255 later tokens at once with the decode rule,
+which computes what 255 single-token steps compute (pinned in tests/test_oracle.py).
+
+Random N(0, 0.02) weights leave the top logits nearly flat (median top-1 / top-2
+margin about 8 bf16 ulps), and 28 layers carry every bf16 rounding forward, so a
+greedy pick is decided by rounding alone at a sizeable share of steps. Measured on
+the CPU: the oracle against itself, sequential single-token steps against the
+teacher-forced batch (the same arithmetic, another fp32 summation order in the
+matrix products), agrees on 58 of 64 steps, and its logits differ by up to 0.14
+(2.9% of the top logit). No implementation that does not copy the oracle's summation
+order can reach 99% agreement here. The test therefore measures that noise in every
+run, from the reference's own two GEMV forms: the one-pass `_dot16` and the split-K
+`_part` / `_reduce` (research/realmodel/int8_linear.py:26-64), each run through the
+whole model. Parity is: every step's GPU logits within twice that noise of the
+oracle's, and greedy agreement with the oracle no worse than the two reference forms'
+agreement with each other, less 3% of the steps. A disagreement is then a near-tie by
+construction: the oracle's margin between its pick and the GPU's is at most twice
+their logit distance. The reference's decoder test compares tokens with generate's
+(research/realmodel/test_fast_decode.py:26-40) on a tiny model, where rounding never
+decides a pick; the tiny-model tests here keep its exact-match bar.
+
+Qwen3-8B: the whole 36-layer model (hidden 4096, intermediate 12288, 32 q / 8 kv heads)
+after an 8192-token prompt, with the cache at 8704 slots, so every step's attention is
+split over 32 blocks per kv head and merged by its own launch. The oracle cannot run
+36 layers of an 8192-token prompt in a test's time, so the full model is checked by
+properties that hold at any size: the fused step against the one-kernel-per-op step
+(logits and K/V within 2e-2), and NaN in every cache slot past the position leaving
+the logits bit-identical (the reference's poisoning test of its split kernel,
+research/phase5/test_graph_gpu.py:250-261). Two layers at the same widths and the same
+8192-token prompt are then checked against the oracle, teacher-forced.
+"""
+
+import pytest
+import torch
+
+from oracle.qwen3 import Qwen3Oracle, Qwen3Shape
+from tests.near_tie import near_tie_bound
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_for(eng, cap):
+    c = eng.cfg
+    shape = Qwen3Shape(c.vocab, c.hidden, c.inter, c.layers, c.heads, c.kv_heads, c.head_dim, c.rope_theta,
+                       c.rms_eps, c.tied)
+    return Qwen3Oracle(shape, eng.weights, dtype=torch.bfloat16, cap=cap)
+
+
+def teacher_forced_logits(orc, prompt, got):
+    """Oracle logits [len(got), vocab] for every greedy step of `got`: the prompt's last row, then got[:-1] fed
+    back at once with the decode rule."""
+    orc.reset()
+    logits = orc.forward(prompt, 0).float()[None]
+    if len(got) > 1:
+        rest = orc.forward(torch.tensor(got[:-1]), len(prompt), all_logits=True, rule='decode').float()
+        logits = torch.cat([logits, rest])
+    return logits
+
+
+def teacher_forced_check(orc, prompt, got):
+    """(agreeing steps, non-near-tie disagreements [(step, oracle pick, got, margin)], oracle logits)."""
+    logits = teacher_forced_logits(orc, prompt, got)
+    picks = logits.argmax(1).tolist()
+    bad = []
+    for i, (p, g) in enumerate(zip(picks, got)):
+        margin = float(logits[i, p] - logits[i, g])
+        if p != g and not margin < near_tie_bound(float(logits[i, p])):
+            bad.append((i, p, g, margin))
+    return sum(p == g for p, g in zip(picks, got)), bad, logits
+
+
+def test_qwen3_1p7b_full_model_256_greedy_tokens_match_oracle():
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    from efficientgpt_amd.qwen3 import QWEN3_1_7B, Qwen3Int8Engine
+    prompt_len, new = 128, 256
+    cap = prompt_len + new
+    eng = Qwen3Int8Engine.random(QWEN3_1_7B, cap, seed=0, keep_weights=True)
+    prompt = torch.randint(0, QWEN3_1_7B.vocab, (prompt_len,), generator=torch.Generator().manual_seed(1))
+    dec = GraphGreedyDecoder(eng, max_cache_len=cap)
+    got, st = dec.generate(prompt.view(1, -1).cuda(), new)
+    assert st['tokens'] == new and len(got) == new
+    assert len(set(got)) > 8, 'degenerate model output would make agreement trivial'
+    # the same decode again with every step's logits kept: prefill, then graph replays
+    eng.reset()
+    gpu = [eng.prefill(prompt).float().cpu()]
+    again = [int(eng.token)]
+    for _ in range(new - 1):
+        eng.replay()
+        again.append(int(eng.token))
+        gpu.append(eng.logits[0].float().cpu())
+    assert again == got  # the decoder's token stream is the graph's
+    gpu = torch.stack(gpu)
+    orc = oracle_for(eng, cap)
+    want = teacher_forced_logits(orc, prompt, got)  # the reference's one-pass GEMV form
+    orc.set_ksplit(2)
+    other = teacher_forced_logits(orc, prompt, got)  # its split-K form (2 chunks) of the same products
+    noise = float((other - want).abs().max())
+    dev = (gpu - want).abs().amax(1)
+    picks, other_picks = want.argmax(1), other.argmax(1)
+    agree = int((picks == torch.tensor(got)).sum())
+    self_agree = int((picks == other_picks).sum())
+    print(f'1.7B: {len(set(got))} distinct tokens; agreement with the oracle {agree}/{new}, the reference\'s two '
+          f'GEMV forms with each other {self_agree}/{new}; max logit distance GPU-oracle {float(dev.max()):.4g}, '
+          f'split-K-oracle {noise:.4g} (top logit {float(want.max()):.3g})', flush=True)
+    assert noise > 0
+    assert float(dev.max()) <= 2 * noise, (float(dev.max()), noise)
+    assert agree >= self_agree - 0.03 * new, (agree, self_agree)
+    for i in range(new):  # each disagreement is within the GPU's distance from the oracle at that step
+        p = int(picks[i])
+        if p != got[i]:
+            assert float(want[i, p] - want[i, got[i]]) <= 2 * float(dev[i]) + 1e-6, i
+
+
+def _qwen3_8b_long_prompt():
+    return torch.randint(0, 151936, (8192,), generator=torch.Generator().manual_seed(3))
+
+
+@pytest.fixture(scope='module')
+def qwen3_8b_long():
+    """The whole Qwen3-8B at 8704 cache slots (the 8192-token prompt plus 512 tokens)."""
+    from efficientgpt_amd.qwen3 import QWEN3_8B, Qwen3Int8Engine
+    eng = Qwen3Int8Engine.random(QWEN3_8B, 8704, seed=0)
+    yield eng
+    del eng
+    torch.cuda.empty_cache()
+
+
+def test_qwen3_8b_full_model_8192_prompt_fused_matches_unfused(qwen3_8b_long):
+    """24 steps past an 8192-token prompt: the fused step (attention split 32 ways per kv head, merged by its own
+    launch) against the one-kernel-per-op step, on the same tokens (the unfused run's picks are fed to every run).
+    Over 36 layers the two forms' different attention summation orders move the logits by several bf16 ulps, so
+    the bound is measured in the same run: the one-kernel-per-op step with its attention split 24 ways instead of
+    32 (the same arithmetic in another order). The fused step may differ from the unfused one by at most twice
+    that (and always passes within 2e-2 of the largest logit); K/V likewise."""
+    eng = qwen3_8b_long
+    assert eng.nsplit > 24, eng.nsplit  # the separate merge launch
+    prompt = _qwen3_8b_long_prompt()
+    steps = 24
+    runs = {}
+    for name, fn, nsplit in (('unfused', eng.step_unfused, eng.nsplit), ('unfused24', eng.step_unfused, 24),
+                             ('fused', eng.step, eng.nsplit)):
+        eng.reset()
+        eng.prefill(prompt)
+        toks, logits = [], []
+        forced = runs.get('unfused', (None,))[0]
+        saved, eng.nsplit = eng.nsplit, nsplit  # the one-kernel-per-op step's attention split count
+        try:
+            for i in range(steps):
+                if forced is not None and i > 0:
+                    eng.token.fill_(forced[i - 1])
+                fn()
+                toks.append(int(eng.token))
+                logits.append(eng.logits[0].float().clone())
+            torch.cuda.synchronize()
+        finally:
+            eng.nsplit = saved
+        runs[name] = (toks, torch.stack(logits), eng.k_cache.clone(), eng.v_cache.clone(), int(eng.position))
+    (tu, lu, ku, vu, pu), (_, la, ka, va, _), (tf, lf, kf, vf, pf) = runs['unfused'], runs['unfused24'], runs['fused']
+    assert pu == pf == len(prompt) + steps
+    top = float(lu.abs().max())
+    noise = float((la - lu).abs().max())
+    dev = float((lf - lu).abs().max())
+    print(f'8B full model: fused vs unfused logits {dev:.4g}, unfused split 24 vs 32 {noise:.4g} (top {top:.3g})',
+          flush=True)
+    assert dev <= max(2e-2 * top, 2 * noise), (dev, noise, top)
+    for u, a, f in ((ku, ka, kf), (vu, va, vf)):
+        assert torch.equal(u[:, :, :len(prompt)], f[:, :, :len(prompt)])  # prompt slots: the same prefill
+        scale = float(u.float().abs().max())
+        kv_noise = float((a.float() - u.float()).abs().max())
+        assert float((u.float() - f.float()).abs().max()) <= max(2e-2 * scale, 2 * kv_noise)
+    assert sum(a == b for a, b in zip(tu, tf)) >= steps - 2, (tu, tf)
+    assert len(set(tu)) > 3
+    del runs, ku, vu, kf, vf, ka, va
+
+
+def test_qwen3_8b_full_model_8192_prompt_ignores_cache_past_position(qwen3_8b_long):
+    """NaN in every slot past the 8192-token prompt leaves 8 fused steps' logits bit-identical: only live slots
+    are read, through the 32-way split and its merge launch, at full depth."""
+    eng = qwen3_8b_long
+    prompt = _qwen3_8b_long_prompt()
+    runs = []
+    for fill in (0.0, float('nan')):
+        eng.reset()
+        eng.prefill(prompt)
+        eng.k_cache[:, :, len(prompt):] = fill
+        eng.v_cache[:, :, len(prompt):] = fill
+        logits = []
+        for _ in range(8):
+            eng.step()
+            logits.append(eng.logits[0].clone())
+        torch.cuda.synchronize()
+        runs.append(logits)
+    assert all(torch.equal(a, b) for a, b in zip(*runs))
+    assert not any(bool(torch.isnan(a.float()).any()) for a in runs[0])
+
+
+def test_qwen3_8b_widths_8192_prompt_match_oracle():
+    """Two layers at Qwen3-8B widths (4 query heads per kv head, o_proj over 4096 inputs, a 4096-token vocabulary
+    to keep the oracle's head small), the 8192-token prompt and the 8704-slot cache: prefill logits and 16 graph
+    replays, teacher-forced against the oracle, every step's logits within 2e-2."""
+    from efficientgpt_amd.qwen3 import Qwen3Config, Qwen3Int8Engine
+    cfg = Qwen3Config(vocab=4096, hidden=4096, inter=12288, layers=2, heads=32, kv_heads=8, head_dim=128,
+                      tied=False)
+    cap, steps = 8704, 16
+    eng = Qwen3Int8Engine.random(cfg, cap, seed=2, std=0.03, keep_weights=True)
+    assert eng.nsplit > 16, eng.nsplit
+    prompt = torch.randint(0, cfg.vocab, (8192,), generator=torch.Generator().manual_seed(4))
+    eng.reset()
+    gpu_logits = [eng.prefill(prompt).float().cpu()]
+    got = [int(eng.token)]
+    for _ in range(steps - 1):
+        eng.replay()
+        got.append(int(eng.token))
+        gpu_logits.append(eng.logits[0].float().cpu())
+    assert int(eng.position) == len(prompt) + steps - 1
+    assert len(set(got)) > 3, got
+    orc = oracle_for(eng, cap)
+    agree, bad, want = teacher_forced_check(orc, prompt, got)
+    print(f'8B widths, 8192-token prompt: agreement {agree}/{steps}, near-tie misses {bad}', flush=True)
+    assert not bad, bad
+    assert agree >= steps - 1, (agree, steps)
+    for i, g in enumerate(gpu_logits):
+        assert float((g - want[i]).abs().max()) <= 2e-2 * float(want[i].abs().max()), i

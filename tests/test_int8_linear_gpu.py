@@ -243,3 +243,16 @@ def test_prefill_op_uses_kernel_and_falls_back_for_unaligned_k():
     y = int8_linear(x.cuda().view(4, 12, 2048), q.cuda(), s.cuda())  # leading dims, kernel path
     assert y.shape == (4, 12, 512)
     check_against_oracle(y.view(48, 512).cpu(), x, q, s)
+
+
+@pytest.mark.parametrize('rows', [1, 3, 40])
+def test_int8_linear_opcheck(rows):
+    """torch.library.opcheck of efficientgpt::int8_linear on device tensors: schema, fake implementation
+    (shape / dtype / device against the real kernel's output) and AOT dispatch, at decode (1, 3 rows: the GEMV)
+    and prefill (40 rows: the GEMM) sizes. The reference pins its fake through torch.compile parity
+    (research/realmodel/test_int8_linear.py:62-79)."""
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, 2048, generator=g).to(torch.bfloat16).cuda()
+    w = torch.randint(-127, 128, (512, 2048), generator=g, dtype=torch.int8).cuda()
+    s = (torch.rand(512, generator=g) * 0.01 + 1e-3).cuda()
+    torch.library.opcheck(torch.ops.efficientgpt.int8_linear.default, (x, w, s))

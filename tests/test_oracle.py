@@ -232,3 +232,134 @@ def test_qwen3_oracle_int8_rule_uses_decode_and_prefill_formulas():
         got = lin(x).float().numpy()
         want = oint8.linear(x.float().numpy(), q.numpy(), s.numpy())
         assert np.array_equal(got, want), rows
+        # the forced decode rule: every row by the single-row formula, whatever the row count
+        forced = lin(x, 'decode').float().numpy()
+        assert np.array_equal(forced, oint8.linear_decode(x.float().numpy(), q.numpy(), s.numpy())), rows
+
+
+# ---------------------------------------------------------------- RoPE frequencies and tables vs transformers
+
+ROPE_CASES = [  # (rope_theta, head_dim, hidden, heads, kv_heads, slots)
+    (1e6, 128, 2048, 16, 8, 4096),   # Qwen3-1.7B
+    (1e6, 128, 4096, 32, 8, 8704),   # Qwen3-8B at the long-context cache
+    (1e4, 32, 128, 4, 2, 256),       # the reference's tiny test model (transformers' default theta)
+]
+
+
+@pytest.mark.parametrize('theta,d,hidden,heads,kv,slots', ROPE_CASES)
+def test_rope_frequencies_and_tables_match_transformers(theta, d, hidden, heads, kv, slots):
+    """default_inv_freq and both rope_tables (the oracle's and the engine's, built on the host) against
+    transformers' Qwen3RotaryEmbedding (compute_default_rope_parameters, then its fp32 forward cast to bf16),
+    bit for bit; a planted wrong theta or a frequency index off by one must differ."""
+    transformers = pytest.importorskip('transformers')
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding
+
+    from efficientgpt_amd.qwen3 import Qwen3Config
+    from efficientgpt_amd.qwen3 import rope_tables as engine_rope_tables
+    from oracle.qwen3 import Qwen3Shape, default_inv_freq, rope_tables
+
+    cfg = transformers.Qwen3Config(vocab_size=512, hidden_size=hidden, intermediate_size=256, num_hidden_layers=1,
+                                   num_attention_heads=heads, num_key_value_heads=kv, head_dim=d, rope_theta=theta,
+                                   max_position_embeddings=slots)
+    rot = Qwen3RotaryEmbedding(cfg)
+    shape = Qwen3Shape(vocab=512, hidden=hidden, inter=256, layers=1, heads=heads, kv_heads=kv, head_dim=d,
+                       rope_theta=theta)
+    inv = default_inv_freq(shape)
+    assert inv.dtype == rot.inv_freq.dtype == torch.float32
+    assert torch.equal(inv, rot.inv_freq)
+    x = torch.zeros(1, 1, d, dtype=torch.bfloat16)
+    want_cos, want_sin = rot(x, torch.arange(slots)[None])
+    cos, sin = rope_tables(shape, slots, torch.bfloat16)
+    assert torch.equal(cos, want_cos[0]) and torch.equal(sin, want_sin[0])
+    ecfg = Qwen3Config.from_hf(cfg)
+    assert ecfg.rope_theta == theta and ecfg.head_dim == d
+    ecos, esin = engine_rope_tables(ecfg, slots)
+    assert torch.equal(ecos, want_cos[0]) and torch.equal(esin, want_sin[0])
+    # planted mistakes: theta off by a factor 10, the exponent's index shifted by one
+    wrong_theta = Qwen3Shape(vocab=512, hidden=hidden, inter=256, layers=1, heads=heads, kv_heads=kv, head_dim=d,
+                             rope_theta=theta * 10)
+    assert not torch.equal(default_inv_freq(wrong_theta), rot.inv_freq)
+    shifted = 1.0 / (theta ** (torch.arange(1, d + 1, 2, dtype=torch.float) / d))
+    assert not torch.equal(shifted, rot.inv_freq)
+    assert not torch.equal(rope_tables(wrong_theta, slots, torch.bfloat16)[0], want_cos[0])
+
+
+# ---------------------------------------------------------------- teacher-forced batch form of the oracle
+
+@pytest.mark.parametrize('shape_name', ['TINY', 'SMALL'])
+def test_oracle_teacher_forced_rows_equal_sequential_decode(shape_name):
+    """forward(tokens, pos, all_logits=True, rule='decode') computes in one pass what len(tokens) single-token
+    decode steps compute. The rows differ from the sequential steps only by fp32 summation order inside the
+    matrix products (one bf16 ulp in an activation, carried through the layers): within 1e-2 of the largest
+    logit, the same greedy pick (a near-tie aside) and the same cache. Planted mistakes move further off: the
+    prefill rule on the 24 rows (double rounding), and positions shifted by one (RoPE and the causal mask).
+    The chunked attention of a long prompt equals the unchunked form within the same bound."""
+    from oracle.qwen3 import TINY, Qwen3Oracle, Qwen3Shape, quantize_weights, random_weights
+    from tests.near_tie import near_tie_bound
+    shape = TINY if shape_name == 'TINY' else Qwen3Shape(vocab=1024, hidden=512, inter=1024, layers=2, heads=16,
+                                                          kv_heads=8, head_dim=128)
+    w = quantize_weights(random_weights(shape, seed=5, std=0.15, norm_jitter=0.1), shape)
+    g = torch.Generator().manual_seed(6)
+    prompt = torch.randint(0, shape.vocab, (40,), generator=g)
+    forced = torch.randint(0, shape.vocab, (24,), generator=g)
+
+    def primed():
+        o = Qwen3Oracle(shape, w, cap=96)
+        o.forward(prompt, 0)
+        return o
+
+    seq = primed()
+    want = torch.stack([seq.forward([int(t)], 40 + i) for i, t in enumerate(forced)]).float()
+    scale = float(want.abs().max())
+    bat = primed()
+    got = bat.forward(forced, 40, all_logits=True, rule='decode').float()
+    rel = float((got - want).abs().max()) / scale
+    assert float((got[0] - want[0]).abs().max()) == 0.0  # the first row sees the same cache in both forms
+    assert rel <= 1e-2, rel
+    for i in range(len(forced)):
+        a, b = int(torch.argmax(got[i])), int(torch.argmax(want[i]))
+        assert a == b or float(want[i, b] - want[i, a]) < near_tie_bound(float(want[i, b])), i
+    for L in range(shape.layers):
+        kb, ks = bat.k_cache[L].float(), seq.k_cache[L].float()
+        assert float((kb - ks).abs().max()) <= 1e-2 * float(ks.abs().max())
+    off_rule = float((primed().forward(forced, 40, all_logits=True).float() - want).abs().max()) / scale
+    off_pos = float((primed().forward(forced, 41, all_logits=True, rule='decode').float() - want).abs().max()) / scale
+    assert off_rule > rel and off_pos > 0.1, (off_rule, off_pos)
+    # chunked attention (chunk 7) against one chunk covering every row
+    l1 = Qwen3Oracle(shape, w, cap=96).forward(prompt, 0, all_logits=True).float()
+    o2 = Qwen3Oracle(shape, w, cap=96)
+    o2._attention = (lambda q, layer, pos0, f=o2._attention: f(q, layer, pos0, chunk=7))
+    l2 = o2.forward(prompt, 0, all_logits=True).float()
+    assert float((l1 - l2).abs().max()) <= 1e-2 * float(l1.abs().max())
+
+
+def test_oracle_splitk_sum_is_another_fp32_order_of_the_same_product():
+    """Linear.ksplit (the reference's split-K GEMV, research/realmodel/int8_linear.py:41-64): chunks of
+    KCHUNK = ceil(ceil(K / splits) / 128) * 128 columns. Pinned by: integer-valued inputs (every fp32 partial sum
+    exact) give the one-pass result bit for bit, whatever the chunking; each chunk boundary matters (zeroing the
+    columns past the first chunk leaves exactly the first chunk's one-pass product, which a boundary anywhere but
+    at 256 would change); random inputs stay within fp32 rounding of
+    the fp64 truth and round to the same bf16 as the one-pass form on all but a few outputs."""
+    from oracle.qwen3 import Linear
+    g = torch.Generator().manual_seed(11)
+    k, n = 300, 96
+    q = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    s = torch.rand(n, generator=g) * 0.01 + 1e-3
+    one, two, three = Linear(qweight=q, scale=s), Linear(qweight=q, scale=s, ksplit=2), \
+        Linear(qweight=q, scale=s, ksplit=3)
+    xi = torch.randint(-8, 9, (4, k), generator=g).to(torch.bfloat16)
+    assert torch.equal(one(xi, 'decode'), two(xi, 'decode')) and torch.equal(one(xi, 'decode'), three(xi, 'decode'))
+    # ksplit 2 at K = 300: KCHUNK = 256, chunks [0, 256) and [256, 300)
+    x = torch.randn(5, k, generator=g).to(torch.bfloat16)
+    two(x, 'decode')  # builds the cached image
+    head = x.clone()
+    head[:, 256:] = 0
+    assert torch.equal(two._sum(head), x[:, :256].float() @ q[:, :256].float().t())
+    assert not torch.equal(two._sum(x), one._sum(x))  # a different order: some sums round differently
+    truth = x.double() @ q.double().t()
+    for lin in (two, three):
+        acc = lin._sum(x).double()
+        bound = k * 2.0 ** -23 * (x.double().abs() @ q.double().abs().t())
+        assert bool(((acc - truth).abs() <= bound).all())
+        same = (lin(x, 'decode') == one(x, 'decode')).float().mean()
+        assert float(same) >= 0.97, float(same)

@@ -361,3 +361,55 @@ def test_engine_from_int8_checkpoint_decodes_identically(tmp_path):
         toks.append((logits, seq))
     assert torch.equal(toks[0][0], toks[1][0])
     assert toks[0][1] == toks[1][1]
+
+
+def _tiny_transformers(attn=None):
+    transformers = pytest.importorskip('transformers')
+    torch.manual_seed(0)
+    kw = {'attn_implementation': attn} if attn else {}
+    cfg = transformers.Qwen3Config(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                                   max_position_embeddings=256, tie_word_embeddings=True, initializer_range=0.2, **kw)
+    return transformers.Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
+
+
+def test_graph_decoder_quantize_opt_in_matches_quantize_model():
+    """A bf16 transformers model is refused without quantize=True (tested on the CPU); with it, the decoder's
+    tokens equal those of the same model quantised by quantize_model first."""
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    from efficientgpt_amd.int8_linear import quantize_model
+    a = _tiny_transformers().cuda()
+    b = _tiny_transformers().cuda()
+    quantize_model(b)
+    x = torch.randint(0, 512, (1, 9), generator=torch.Generator().manual_seed(8)).cuda()
+    got, _ = GraphGreedyDecoder(a, max_cache_len=64, quantize=True).generate(x, 30)
+    want, _ = GraphGreedyDecoder(b, max_cache_len=64).generate(x, 30)
+    assert got == want
+    assert len(set(got)) > 8
+
+
+def test_hf_adapter_batch_of_two_and_left_padding():
+    """transformers generate() with attn_implementation 'egpt_decode': an unpadded batch of two equals each row
+    decoded alone by eager SDPA attention within the near-tie rule; a left-padded batch raises ValueError (the
+    kernel reads cache slots 0..position and cannot mask padding) instead of attending the pad slots."""
+    transformers = pytest.importorskip('transformers')
+    from efficientgpt_amd import hf
+    hf.register()
+    model = _tiny_transformers(hf.NAME).cuda()
+    ref = _tiny_transformers('sdpa').cuda()
+    x = torch.randint(0, 512, (2, 7), generator=torch.Generator().manual_seed(9)).cuda()
+    kw = dict(max_new_tokens=16, min_new_tokens=16, do_sample=False, pad_token_id=0)
+    with torch.no_grad():
+        got = model.generate(input_ids=x, attention_mask=torch.ones_like(x), **kw)[:, 7:].tolist()
+        for row in range(2):
+            out = ref.generate(input_ids=x[row:row + 1], attention_mask=torch.ones_like(x[row:row + 1]),
+                               output_scores=True, return_dict_in_generate=True, **kw)
+            want = out.sequences[0, 7:].tolist()
+            if got[row] != want:  # free-running decodes may part at a near-tie of the two attention forms
+                i = next(j for j, (p, q) in enumerate(zip(got[row], want)) if p != q)
+                top = out.scores[i][0].float().topk(2).values
+                assert float(top[0] - top[1]) < near_tie_bound(float(top[0])), (row, i)
+        mask = torch.ones_like(x)
+        mask[0, :2] = 0
+        with pytest.raises(ValueError, match='padd'):
+            model.generate(input_ids=x, attention_mask=mask, **kw)
