@@ -14,6 +14,8 @@ LIB_PATH = Path(__file__).resolve().parent / 'libegpt_hip.so'
 
 EGPT_OK = 0
 EGPT_ERR_UNSUPPORTED = -2
+EGPT_ERR_WORKSPACE = -4
+NOALLOC_SCRATCH_BYTES = 4 << 20  # EGPT_NOALLOC_SCRATCH_BYTES
 EGPT_F32, EGPT_BF16, EGPT_F16 = 0, 1, 2
 ABI_VERSION = 1
 
@@ -43,6 +45,13 @@ SIGNATURES = {
                                   _c_vp, _c_i64, _c_i64,
                                   _c_vp, _c_size,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp]),
+    'egpt_decode_attn_noalloc': (_c_int, [_c_int,
+                                          _c_vp, _c_i64, _c_i64,
+                                          _c_vp, _c_i64, _c_i64, _c_i64,
+                                          _c_vp, _c_i64, _c_i64, _c_i64,
+                                          _c_vp, _c_i64,
+                                          _c_vp, _c_i64, _c_i64,
+                                          _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp]),
     'egpt_rmsnorm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_f, _c_vp]),
     'egpt_add_rmsnorm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_f, _c_vp]),
     'egpt_qk_norm_rope': (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp,

@@ -8,6 +8,8 @@
 // every K/V byte is read once. A second kernel merges the per-split partial
 // softmax states. The arithmetic lives in attn_core.h; its summation order
 // differs from SDPA, so results are not bit-exact against it.
+#include <mutex>
+
 #include "attn_core.h"
 
 namespace egpt {
@@ -204,4 +206,61 @@ extern "C" int egpt_decode_attn(int dtype, const void* q, int64_t q_sb, int64_t 
     case EGPT_F16: return dispatch_dim<_Float16>(a, D, stream);
     default: return dispatch_dim<float>(a, D, stream);
   }
+}
+
+// ---------------------------------------------------------------------------
+// The same attention with no allocation at all: the split partials live in a
+// file-scope device array instead of a caller's workspace. Each device holds its
+// own copy of the array at its own address; the host learns that address once per
+// device (hipGetSymbolAddress, with the device current) and passes it to the
+// kernels like any workspace. The array's name is never used as a device address
+// on the host. Every split writes its own partial before the combine reads it, so
+// nothing in the array has to start at zero; calls that overlap on one device
+// share the array and race.
+namespace egpt {
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[EGPT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// The scratch array's address on the current device, looked up on its first use there.
+int scratch_on_current_device(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return EGPT_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return EGPT_ERR_UNSUPPORTED;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) return EGPT_ERR_INVALID;
+    if (sdev != dev) return EGPT_ERR_INVALID;  // the array's address is per device: launch with its device current
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev]) return EGPT_ERR_LAUNCH;
+  *ptr = g_scratch_ptr[dev];
+  return EGPT_OK;
+}
+
+}  // namespace
+}  // namespace egpt
+
+extern "C" int egpt_decode_attn_noalloc(int dtype, const void* q, int64_t q_sb, int64_t q_sh, const void* k,
+                                        int64_t k_sb, int64_t k_sh, int64_t k_sn, const void* v, int64_t v_sb,
+                                        int64_t v_sh, int64_t v_sn, const int64_t* position, int64_t pos_stride,
+                                        void* out, int64_t o_sb, int64_t o_sh, int B, int Hq, int Hkv, int cap, int D,
+                                        int nsplit, float scale, hipStream_t stream) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || cap < 1 || D < 1) return EGPT_ERR_INVALID;
+  if (nsplit <= 0) nsplit = egpt_decode_attn_default_splits(B, Hkv, cap);
+  if (attn_workspace_bytes(B, Hq, D, nsplit) > EGPT_NOALLOC_SCRATCH_BYTES) return EGPT_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int st = scratch_on_current_device(stream, &ws);
+  if (st != EGPT_OK) return st;
+  return egpt_decode_attn(dtype, q, q_sb, q_sh, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn, position, pos_stride, out,
+                          o_sb, o_sh, ws, EGPT_NOALLOC_SCRATCH_BYTES, B, Hq, Hkv, cap, D, nsplit, scale, stream);
 }

@@ -109,6 +109,30 @@ int egpt_decode_attn(int dtype,
                      hipStream_t stream);
 
 /*
+ * egpt_decode_attn without a workspace and without any allocation: the split
+ * partials go to a scratch array that the library holds in device memory, one copy
+ * per device, for the life of the process. No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments and result as
+ * egpt_decode_attn minus the workspace. Limits: the partials of B * Hq * nsplit
+ * (query row, split) pairs, egpt_decode_attn_workspace bytes, must fit in
+ * EGPT_NOALLOC_SCRATCH_BYTES (else EGPT_ERR_WORKSPACE: at D 128, 8,065 pairs, e.g.
+ * 16 query heads x 504 splits). The device that runs the call must be current
+ * (EGPT_ERR_INVALID if `stream` belongs to another). Calls that overlap on one
+ * device share the array and race; the first call on a device looks up the array's
+ * address there, so make it before a graph capture.
+ */
+#define EGPT_NOALLOC_SCRATCH_BYTES (4u << 20)
+int egpt_decode_attn_noalloc(int dtype,
+                             const void *q, int64_t q_sb, int64_t q_sh,
+                             const void *k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                             const void *v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                             const int64_t *position, int64_t pos_stride,
+                             void *out, int64_t o_sb, int64_t o_sh,
+                             int B, int Hq, int Hkv, int cap, int D, int nsplit, float scale,
+                             hipStream_t stream);
+
+/*
  * Decode-step kernels of the Qwen3 layer around the two hot kernels. They replace
  * the elementwise work the reference leaves to transformers' modules compiled by
  * Inductor inside its graph step (research/realmodel/fast_decode.py:42-49); the

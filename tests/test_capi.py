@@ -49,6 +49,11 @@ def test_argument_errors_return_status_without_launching():
     assert lib.egpt_decode_attn(1, *args, None, 0, 1, 8, 4, 64, 128, 1, 0.1, None) == -4
     assert lib.egpt_decode_attn_workspace(1, 16, 8, 4096, 128, 8, ctypes.byref(size)) == 0
     assert size.value >= 16 * 8 * (128 + 2) * 4
+    # the allocation-free form: more partials than its scratch array holds (16 heads x 505 splits at D 128)
+    assert lib.egpt_decode_attn_workspace(1, 16, 8, 4096, 128, 505, ctypes.byref(size)) == 0
+    assert size.value > _lib.NOALLOC_SCRATCH_BYTES
+    assert lib.egpt_decode_attn_noalloc(1, *args, 1, 16, 8, 4096, 128, 505, 0.1, None) == -4
+    assert lib.egpt_decode_attn_noalloc(1, *args, 0, 16, 8, 4096, 128, 1, 0.1, None) == -1
 
 
 @pytest.mark.parametrize('b,hkv,cap', [(1, 8, 256), (1, 8, 32768), (16, 6, 128), (1, 1, 1)])
