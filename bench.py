@@ -6,9 +6,7 @@ tied embeddings, RoPE theta 1e6), every linear int8 weight-only with
 per-output-channel scales, weights N(0, 0.02); a 128-token uniform-random prompt
 is prefilled, then each step is one replay of the captured decode graph
 (embedding through argmax and the token / position update) producing one token.
-`--model qwen3-8b --prompt 8192` runs the long-context 8B workload instead;
-`--step persistent` times the one-launch persistent step instead of the default
-launch-per-phase step (same tokens; it is the slower form on the MI355X).
+`--model qwen3-8b --prompt 8192` runs the long-context 8B workload instead.
 Weights, cache and prompt are resident in HBM before timing starts.
 
 Prints one JSON line:
@@ -61,8 +59,6 @@ def parse():
     ap.add_argument('--cpu-tokens', type=int, default=8, help='decode steps in the CPU baseline sample (0: skip)')
     ap.add_argument('--no-stream', action='store_true', help='skip the streamed generate() measurement')
     ap.add_argument('--no-extra', action='store_true', help='skip the attention and copy measurements')
-    ap.add_argument('--step', choices=('fused', 'persistent'), default='fused',
-                    help='decode step form: five launches per layer (default) or one persistent launch per token')
     ap.add_argument('--dispatch-grid', action='store_true',
                     help='instead of the decode benchmark: single-pass against default split-K decode attention over '
                          'batch x heads x cache length (one JSON line per point), the data behind the split policy')
@@ -400,8 +396,7 @@ def main():
     cap = args.prompt + max(args.warmup + args.steps, n_stream) + 8
     t = time.perf_counter()
     want_cpu = args.cpu_tokens > 0 and args.model == 'qwen3-1.7b'
-    eng = Qwen3Int8Engine.random(cfg, cap, seed=args.seed, device=dev, persistent=args.step == 'persistent',
-                                 keep_weights=want_cpu)
+    eng = Qwen3Int8Engine.random(cfg, cap, seed=args.seed, device=dev, keep_weights=want_cpu)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t
     prompt = torch.randint(0, cfg.vocab, (args.prompt,), generator=torch.Generator().manual_seed(args.seed + 1))
@@ -426,7 +421,6 @@ def main():
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         gpu_s = e0.elapsed_time(e1) / 1e3
-        eng.check_status()
         value = args.steps / wall
         mean_len = args.prompt + args.warmup + (args.steps + 1) / 2
 
@@ -475,9 +469,8 @@ def main():
         'cpu_baseline': cpu,
         'step': {'bytes': int(step_bytes), 'achieved_gbps': round(step_bytes / step_s / 1e9, 1),
                  'frac': round(step_bytes / step_s / 1e9 / HBM_PEAK_GBPS, 4), 'mean_kv_len': mean_len,
-                 'launches': 1 if eng.persistent else cfg.layers * (5 if eng.nsplit <= 16 else 6) + 2,
-                 'form': 'persistent (egpt_qwen3_persistent_step)' if eng.persistent
-                 else 'fused, one launch per phase (egpt_qwen3_decode_step)'},
+                 'launches': cfg.layers * (5 if eng.nsplit <= 16 else 6) + 2,
+                 'form': 'fused, one launch per phase (egpt_qwen3_decode_step)'},
         'prefill_s': round(prefill_s, 3),
         'streamed_generate': stream,
         'build_s': round(build_s, 1),

@@ -66,10 +66,6 @@ SIGNATURES = {
     'egpt_int8_gemv_fused_parts': (_c_int, [_c_vp, ctypes.POINTER(_c_int)]),
     'egpt_int8_gemv_fused': (_c_int, [_c_vp, _c_vp]),
     'egpt_argmax_parts': (_c_int, [_c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
-    'egpt_qwen3_persistent_supported': (_c_int, [_c_vp]),
-    'egpt_qwen3_persistent_setup': (_c_int, [_c_vp, _c_vp]),
-    'egpt_qwen3_persistent_step': (_c_int, [_c_vp, _c_vp]),
-    'egpt_qwen3_persistent_status': (_c_int, [_c_vp, ctypes.POINTER(ctypes.c_uint32)]),
 }
 
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3

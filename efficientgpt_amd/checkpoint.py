@@ -88,16 +88,27 @@ def load_int8(path, device='cpu'):
     return cfg, packed, inv_freq
 
 
+def _expect(what, t, dtype, shape):
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape):
+        raise ValueError(f'{what}: {t.dtype} {tuple(t.shape)}, expected {dtype} {tuple(shape)}')
+
+
 def _check(cfg, packed):
-    """Shapes and dtypes against the config: a truncated or mismatched file fails here, not in a kernel."""
+    """Every stored tensor's dtype and shape against the config: a truncated or mismatched file fails here, not in a
+    kernel that would read past the end of a short tensor."""
     d, hq, hkv = cfg.head_dim, cfg.heads, cfg.kv_heads
     want = {'qkv_q': ((hq + 2 * hkv) * d, cfg.hidden), 'o_q': (cfg.hidden, hq * d), 'gu_q': (2 * cfg.inter, cfg.hidden),
             'down_q': (cfg.hidden, cfg.inter)}
+    norms = {'in_w': cfg.hidden, 'post_w': cfg.hidden, 'qn_w': d, 'kn_w': d}
+    if len(packed['layers']) != cfg.layers:
+        raise ValueError(f'{len(packed["layers"])} layers stored, the config has {cfg.layers}')
     for i, L in enumerate(packed['layers']):
         for key, shape in want.items():
-            q, s = L[key], L[key[:-1] + 's']
-            if q.dtype != torch.int8 or tuple(q.shape) != shape or s.dtype != torch.float32 or s.shape != (shape[0],):
-                raise ValueError(f'layer {i} {key}: {q.dtype} {tuple(q.shape)} / {s.dtype} {tuple(s.shape)}, '
-                                 f'expected int8 {shape} / float32 ({shape[0]},)')
-    if tuple(packed['embed'].shape) != (cfg.vocab, cfg.hidden) or packed['head_q'].shape != (cfg.vocab, cfg.hidden):
-        raise ValueError('embedding / lm_head shape does not match the config')
+            _expect(f'layer {i} {key}', L[key], torch.int8, shape)
+            _expect(f'layer {i} {key[:-1]}s', L[key[:-1] + 's'], torch.float32, (shape[0],))
+        for key, n in norms.items():
+            _expect(f'layer {i} {key}', L[key], torch.bfloat16, (n,))
+    _expect('embed', packed['embed'], torch.bfloat16, (cfg.vocab, cfg.hidden))
+    _expect('final_norm', packed['norm_w'], torch.bfloat16, (cfg.hidden,))
+    _expect('lm_head qweight', packed['head_q'], torch.int8, (cfg.vocab, cfg.hidden))
+    _expect('lm_head scale', packed['head_s'], torch.float32, (cfg.vocab,))

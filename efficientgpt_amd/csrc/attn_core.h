@@ -214,11 +214,8 @@ __device__ __forceinline__ void attn_mac(const AttnPipe<LPR, U>& pp, const float
 // slot gives the empty state (m = -inf, l = 0, acc = 0). With `out` set (one
 // split covering every live slot) the block writes the attention output itself,
 // out[g * o_sh + d] = acc / l, instead of the partials: the value the combine
-// would compute, whose single weight exp(m - m) is 1. With `tout` set instead,
-// that output goes to 32-bit words tout[g * o_sh + d] = (ttag << 16) | bf16 bits,
-// stored with agent-scope relaxed atomics: the epoch-tagged form in which
-// blocks of one persistent launch hand rows to each other. Must be called by
-// all NT threads of the block.
+// would compute, whose single weight exp(m - m) is 1. Must be called by all NT
+// threads of the block.
 template <typename Geo, typename T, int G, int LPR, int U>
 __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], AttnPipe<LPR, U>& pp,
                                              const T* __restrict__ kbase, int64_t k_sn, const T* __restrict__ vbase,
@@ -226,8 +223,7 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
                                              float* __restrict__ ws_m, float* __restrict__ ws_l,
                                              float* __restrict__ ws_acc, int64_t row, int nsplit,
                                              bool xnew = false, const float* xk = nullptr, const float* xv = nullptr,
-                                             T* __restrict__ out = nullptr, int64_t o_sh = 0,
-                                             uint32_t* __restrict__ tout = nullptr, uint32_t ttag = 0) {
+                                             T* __restrict__ out = nullptr, int64_t o_sh = 0) {
   constexpr int EPL = Geo::EPL;
   constexpr int EPV = Geo::EPV;
   constexpr int LPS = Geo::LPS;
@@ -372,11 +368,6 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
     }
     if (out) {
       Elem<T>::store1(out + (int64_t)g * o_sh + d, a / ls);
-      continue;
-    }
-    if (tout) {
-      __hip_atomic_store((global_ptr<uint32_t>)(tout + (int64_t)g * o_sh + d),
-                         (ttag << 16) | (uint32_t)f32_to_bf16(a / ls), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       continue;
     }
     const int64_t slot = row + (int64_t)g * nsplit;

@@ -465,7 +465,7 @@ __global__ __launch_bounds__(kFThreads) void argmax_final_kernel(const float* __
   for (int j = threadIdx.x; j < parts; j += kFThreads) best = arg_better(best, ArgBest{part_v[j], part_i[j]});
   best = block_argbest<kFWaves>(best);
   if (threadIdx.x == 0) {
-    *token = best.i == 0x7fffffff ? 0 : best.i;  // all-NaN logits: token 0
+    *token = best.i == 0x7fffffff ? 0 : best.i;  // no logits at all: token 0
     if (position) *position += 1;
   }
 }
@@ -880,7 +880,6 @@ void step_gemvs(const egpt_qwen3_step* s, egpt_gemv_fused* out) {
 
 size_t fused_step_bytes(const egpt_qwen3_step* s) { return step_layout(s).total; }
 int qwen3_check_step(const egpt_qwen3_step* s) { return check_step(s); }
-size_t persistent_step_bytes(const egpt_qwen3_step* s);  // qwen3_persistent.hip
 
 }  // namespace egpt
 
@@ -929,8 +928,7 @@ extern "C" int egpt_qwen3_step_default_splits(int heads, int kv_heads, int head_
 extern "C" int egpt_qwen3_step_workspace(const egpt_qwen3_step* s, size_t* bytes) {
   if (!s || !bytes || s->heads < 1 || s->kv_heads < 1 || s->nsplit < 1 || s->head_dim < 1 || s->vocab < 1)
     return EGPT_ERR_INVALID;
-  // the launch-per-phase step's region, then the persistent step's (qwen3_persistent.hip)
-  *bytes = (step_layout(s).total + 255) / 256 * 256 + persistent_step_bytes(s);
+  *bytes = (step_layout(s).total + 255) / 256 * 256;
   return EGPT_OK;
 }
 

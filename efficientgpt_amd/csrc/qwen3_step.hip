@@ -9,7 +9,7 @@
 //   argmax       first index of the largest logit (torch.argmax), next token + position
 //                advance of the reference's graph step (research/realmodel/fast_decode.py:45-49)
 // All activations are bf16 stored as uint16.
-#include "common.h"
+#include "step_core.h"
 
 namespace egpt {
 namespace {
@@ -152,17 +152,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
     out[row * ld_out + i] = table[t * ld_table + i];
 }
 
-// argmax, stage 1: each block reduces a contiguous range to (max, first index).
-// A logit compares larger if greater, or equal with a smaller index.
-struct ArgBest {
-  float v;
-  int i;
-};
-
-__device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
-  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
-  return a;
-}
+// argmax, stage 1: each block reduces a contiguous range to (max, first index),
+// in torch.argmax's order (step_core.h arg_better: NaN above every number).
 
 __device__ __forceinline__ ArgBest wave_arg(ArgBest x) {
 #pragma unroll
@@ -215,7 +206,7 @@ __global__ __launch_bounds__(kArgThreads) void argmax_final_kernel(const float* 
   for (int j = threadIdx.x; j < parts; j += kArgThreads) best = arg_better(best, ArgBest{pv[j], pi[j]});
   best = block_arg(best);
   if (threadIdx.x == 0) {
-    *token = best.i == 0x7fffffff ? 0 : best.i;  // all-NaN logits: token 0
+    *token = best.i == 0x7fffffff ? 0 : best.i;  // no logits at all: token 0
     if (position) *position += 1;
   }
 }

@@ -1,7 +1,6 @@
-// Device helpers of the fused decode-step kernels (qwen3_fused.hip, qwen3_persistent.hip):
-// the int8 x bf16 dot product of the GEMV tiles, bf16 unpacking, the greedy
-// (argmax) reduction and the per-head RMSNorm + RoPE of queries and keys. Both
-// kernels use these same functions, so their arithmetic is identical.
+// Device helpers of the fused decode-step kernels (qwen3_fused.hip): the int8 x
+// bf16 dot product of the GEMV tiles, bf16 unpacking, the greedy (argmax)
+// reduction and the per-head RMSNorm + RoPE of queries and keys.
 #pragma once
 
 #include "attn_core.h"
@@ -38,9 +37,12 @@ struct ArgBest {
   int i;
 };
 
-// larger value wins; equal values: the smaller index (torch.argmax's first maximum)
+// torch.argmax's order: NaN ranks above every number, then the larger value;
+// ties (NaN against NaN included) go to the smaller index.
 __device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
-  return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
+  const bool an = a.v != a.v, bn = b.v != b.v;
+  const bool b_wins = an ? (bn && b.i < a.i) : (bn || b.v > a.v || (b.v == a.v && b.i < a.i));
+  return b_wins ? b : a;
 }
 
 template <int W>

@@ -38,12 +38,6 @@ from .int8_linear import MAX_DECODE_ROWS, int8_gemm, quantize_weight
 
 # Prompts longer than this take the library-GEMM attention in prefill.
 PREFILL_KERNEL_MAX_ROWS = 64
-# The persistent step attends with one block per kv head; longer caches keep the
-# launch-per-phase step, whose attention splits every kv head over many blocks.
-PERSISTENT_MAX_CACHE = 4096
-# Whether engines take the persistent step unless told otherwise: off while the
-# launch-per-phase step is the faster of the two on the MI355X.
-PERSISTENT_DEFAULT = False
 
 LINEARS = ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj', 'self_attn.o_proj',
            'mlp.gate_proj', 'mlp.up_proj', 'mlp.down_proj')
@@ -155,7 +149,7 @@ class Qwen3Int8Engine:
     the packed layout pack_qwen3 returns (what efficientgpt_amd.checkpoint stores).
     """
 
-    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False, persistent=None):
+    def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False):
         if max_cache_len < 1:
             raise ValueError('max_cache_len must be >= 1')
         self.cfg = cfg
@@ -174,9 +168,9 @@ class Qwen3Int8Engine:
         self.head_q, self.head_s = put(pk['head_q']), put(pk['head_s'], torch.float32)
         self.inv_freq = None if inv_freq is None else inv_freq.detach().float().cpu()
         del pk
-        self._init_state(int(max_cache_len), persistent)
+        self._init_state(int(max_cache_len))
 
-    def _init_state(self, cap, persistent):
+    def _init_state(self, cap):
         """Everything that depends on the cache capacity: RoPE tables, the K/V cache, the token / position state,
         activation rows, workspaces and the fused step's descriptor. The weights are not touched."""
         c, dev, bf = self.cfg, self.device, torch.bfloat16
@@ -209,10 +203,9 @@ class Qwen3Int8Engine:
         _lib.check('egpt_argmax_workspace', lib.egpt_argmax_workspace(c.vocab, need))
         self.arg_ws = torch.zeros(need.value, device=dev, dtype=torch.uint8)
         self._build_step_desc()
-        self.persistent = self._choose_persistent(persistent)
         self.graph = None
 
-    def with_capacity(self, max_cache_len, persistent=None):
+    def with_capacity(self, max_cache_len):
         """An engine over the same weight tensors (shared, not copied) with its own cache of max_cache_len slots,
         its own state and its own graph: one per capacity bucket of a decoder pool."""
         if max_cache_len < 1:
@@ -223,28 +216,8 @@ class Qwen3Int8Engine:
         other.head_q, other.head_s, other.inv_freq = self.head_q, self.head_s, self.inv_freq
         if hasattr(self, 'weights'):
             other.weights = self.weights
-        other._init_state(int(max_cache_len), persistent)
+        other._init_state(int(max_cache_len))
         return other
-
-    def _choose_persistent(self, want):
-        """Whether step() is the one-launch persistent step (egpt_qwen3_persistent_step).
-
-        want True: required (raises if the library has no persistent kernel for this shape on this device);
-        None: when PERSISTENT_DEFAULT is set, the library supports it and the cache is short enough for its
-        one-split attention; False: the launch-per-phase step."""
-        if want is False or (want is None and not PERSISTENT_DEFAULT):
-            return False
-        lib = _lib.lib()
-        st = lib.egpt_qwen3_persistent_supported(ctypes.byref(self._step_c))
-        if st != _lib.EGPT_OK:
-            if want:
-                _lib.check('egpt_qwen3_persistent_supported', st)
-            return False
-        if want is None and self.cap > PERSISTENT_MAX_CACHE:
-            return False
-        _lib.check('egpt_qwen3_persistent_setup', lib.egpt_qwen3_persistent_setup(ctypes.byref(self._step_c),
-                                                                                  self._stream()))
-        return True
 
     def _build_step_desc(self):
         """The egpt_qwen3_step descriptor of the fused decode step (pointers into this engine's tensors)."""
@@ -280,15 +253,15 @@ class Qwen3Int8Engine:
     # ------------------------------------------------------------------ construction helpers
 
     @classmethod
-    def from_int8(cls, path, max_cache_len, device='cuda', persistent=None):
+    def from_int8(cls, path, max_cache_len, device='cuda'):
         """Engine over an efficientgpt_amd.checkpoint file: the stored int8 layout, no re-quantisation."""
         from .checkpoint import load_int8
         cfg, packed, inv_freq = load_int8(path)
-        return cls(cfg, packed, max_cache_len, device=device, inv_freq=inv_freq, packed=True, persistent=persistent)
+        return cls(cfg, packed, max_cache_len, device=device, inv_freq=inv_freq, packed=True)
 
     @classmethod
     @torch.no_grad()
-    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda', persistent=None, keep_weights=False):
+    def random(cls, cfg, max_cache_len, seed=0, std=0.02, device='cuda', keep_weights=False):
         """Random-init weights N(0, std) (bf16, norms 1), quantised per output channel on the device.
 
         keep_weights: also keep a HOST copy of the transformers-named int8 weights as `.weights` (what a CPU
@@ -321,7 +294,7 @@ class Qwen3Int8Engine:
             w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(randn(c.vocab, c.hidden))
         else:
             w['lm_head.qweight'], w['lm_head.scale'] = quantize_weight(w['model.embed_tokens.weight'])
-        eng = cls(cfg, w, max_cache_len, device=dev, persistent=persistent)
+        eng = cls(cfg, w, max_cache_len, device=dev)
         if keep_weights:
             eng.weights = {k: v.cpu() for k, v in w.items()}
         del w
@@ -456,35 +429,10 @@ class Qwen3Int8Engine:
 
     @torch.inference_mode()
     def step(self):
-        """One decode step on the current stream: consumes self.token at self.position, writes the next token.
-
-        The persistent step (one launch) when self.persistent, else the fused launch-per-phase step."""
-        if self.persistent:
-            self.step_persistent()
-        else:
-            self.step_fused()
-
-    @torch.inference_mode()
-    def step_fused(self):
-        """The fused step (egpt_qwen3_decode_step): five launches per layer and one for the head."""
+        """One decode step on the current stream (egpt_qwen3_decode_step): consumes self.token at self.position,
+        writes the next token; five launches per layer and one for the head."""
         _lib.check('egpt_qwen3_decode_step', _lib.lib().egpt_qwen3_decode_step(ctypes.byref(self._step_c),
                                                                                self._stream()))
-
-    @torch.inference_mode()
-    def step_persistent(self):
-        """The whole step as one persistent launch (egpt_qwen3_persistent_step)."""
-        _lib.check('egpt_qwen3_persistent_step', _lib.lib().egpt_qwen3_persistent_step(ctypes.byref(self._step_c),
-                                                                                       self._stream()))
-
-    def check_status(self):
-        """Raise if any persistent step so far ran out a wait bound (synchronises with the device)."""
-        if not self.persistent:
-            return
-        st = ctypes.c_uint32()
-        _lib.check('egpt_qwen3_persistent_status', _lib.lib().egpt_qwen3_persistent_status(
-            ctypes.byref(self._step_c), ctypes.byref(st)))
-        if st.value:
-            raise RuntimeError(f'persistent decode step failed (status {st.value:#x}): a block waited past its bound')
 
     @torch.inference_mode()
     def step_unfused(self):

@@ -313,35 +313,6 @@ int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
 int egpt_qwen3_step_default_splits(int heads, int kv_heads, int head_dim, int cap);
 int egpt_qwen3_decode_step(const egpt_qwen3_step *step, hipStream_t stream);
 
-/*
- * The same decode step as ONE persistent launch (one 8-wavefront block per CU):
- * the blocks stay resident for the whole step and hand each phase's rows to the
- * next through epoch-tagged words in the workspace, each wavefront streaming its
- * next GEMV tiles while it waits. On the MI355X it is slower than
- * egpt_qwen3_decode_step (hand-offs under load cost more than launch boundaries);
- * it is kept as a tested alternative. Same contract as egpt_qwen3_decode_step (token,
- * position, K/V slot, logits when non-NULL), with the attention of every layer in
- * one split per kv head. Replaces the same reference step
- * (research/realmodel/fast_decode.py:45-49).
- *
- * egpt_qwen3_persistent_supported: EGPT_OK when this model shape and the current
- *   device have a persistent kernel (Qwen3-1.7B widths: hidden 2048, inter 6144,
- *   16 q / 8 kv heads of 128), else EGPT_ERR_UNSUPPORTED.
- * egpt_qwen3_persistent_setup: copies the layer table into the workspace and waits
- *   for the copy (not capturable); call once, and again whenever a pointer of the
- *   descriptor changes. The step refuses (EGPT_ERR_INVALID) a descriptor whose
- *   table was not set up.
- * egpt_qwen3_persistent_step: the launch (capturable; no allocation, no host sync).
- * egpt_qwen3_persistent_status: reads the sticky status word (synchronous): bit 0
- *   is set if a step's wait for another block ran out its bound, in which case
- *   that step also stored token -1.
- * The workspace is egpt_qwen3_step_workspace's (it covers both forms), zeroed once.
- */
-int egpt_qwen3_persistent_supported(const egpt_qwen3_step *step);
-int egpt_qwen3_persistent_setup(const egpt_qwen3_step *step, hipStream_t stream);
-int egpt_qwen3_persistent_step(const egpt_qwen3_step *step, hipStream_t stream);
-int egpt_qwen3_persistent_status(const egpt_qwen3_step *step, uint32_t *status);
-
 /* The step's fused GEMV launches as egpt_gemv_fused descriptions, in launch
  * order (4 per layer, then the head): *count = 4 layers + 1; `out` (capacity
  * entries) may be NULL to query the count. Replaying them through

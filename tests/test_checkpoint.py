@@ -53,3 +53,27 @@ def test_foreign_and_mismatched_files_are_refused(tmp_path):
     checkpoint.save_int8(bad, CFG, pk)
     with pytest.raises(ValueError, match='layer 1 o_q'):
         checkpoint.load_int8(bad)
+
+
+@pytest.mark.parametrize('key,cut', [('q_norm', 'qn_w'), ('post_norm', 'post_w'), ('final', None), ('head_s', None),
+                                     ('embed_dtype', None)])
+def test_every_stored_tensor_is_checked(tmp_path, key, cut):
+    """Norm vectors, the final norm, the head's scales and the embedding's dtype are checked against the config
+    too, so a short or mistyped tensor never reaches a kernel."""
+    pk = pack_qwen3(CFG, quantize_weights(random_weights(TINY, seed=4, std=0.2), TINY))
+    if cut:
+        pk['layers'][0][cut] = pk['layers'][0][cut][:-8].contiguous()
+        match = f'layer 0 {cut}'
+    elif key == 'final':
+        pk['norm_w'] = pk['norm_w'][:-8].contiguous()
+        match = 'final_norm'
+    elif key == 'head_s':
+        pk['head_s'] = pk['head_s'][:-1].contiguous()
+        match = 'lm_head scale'
+    else:
+        pk['embed'] = pk['embed'].float()
+        match = 'embed'
+    bad = os.path.join(tmp_path, 'bad.safetensors')
+    checkpoint.save_int8(bad, CFG, pk)
+    with pytest.raises(ValueError, match=match):
+        checkpoint.load_int8(bad)
