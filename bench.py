@@ -22,12 +22,20 @@ Prints one JSON line:
   attention_by_length  the same at L = 256 ... 16384
   gemv_1x2048_6144     the reference's headline GEMV shape through egpt_int8_gemv, cold
   prefill_gemm         the MFMA prefill GEMM at the model's shapes, beside the reference's formula
+  launch_floor_us the fixed cost of one dependent GEMV launch in a graph (a one-row GEMV
+                  whose 2 KB of weights come from HBM); `frac_beyond_floor` beside a small
+                  kernel's `frac` takes one floor per launch out of its time
+  gemv_small_batch     egpt_int8_gemv at each Qwen3-1.7B GEMV shape and the lm_head with
+                  1, 2, 4 and 8 activation rows, cold
+  long_context    the Qwen3-8B workload: 8192-token prompt, cache of 8704 slots, graph
+                  replays timed, its GEMV launches timed on their own
   step            the whole step: weight + scale + KV bytes per token / ms per token
   copy_gbps       a device-to-device copy of 1 GiB, the measured bandwidth ceiling
   cpu_baseline    the CPU oracle (oracle/qwen3.py, torch on the host) on a bounded
-                  sample of the same workload: prefill of the same prompt, then a few
-                  greedy decode steps, on the same weights; `kernels` holds the
-                  reference's CPU forms of the GEMV and the attention timed on the host
+                  sample of the same workload: prefill of the same prompt, then 32
+                  greedy tokens (--cpu-tokens; 256 is the whole decode), on the same
+                  weights; `kernels` holds the reference's CPU forms of the GEMV (every
+                  shape, 1-8 rows) and the attention (every cache length) timed on the host
 """
 
 import argparse
@@ -56,7 +64,10 @@ def parse():
     ap.add_argument('--model', choices=('qwen3-1.7b', 'qwen3-8b'), default='qwen3-1.7b')
     ap.add_argument('--prompt', type=int, default=128)
     ap.add_argument('--seed', type=int, default=0)
-    ap.add_argument('--cpu-tokens', type=int, default=8, help='decode steps in the CPU baseline sample (0: skip)')
+    ap.add_argument('--cpu-tokens', type=int, default=32,
+                    help='greedy tokens in the CPU baseline sample (0: skip; 256 is the full decode of the workload)')
+    ap.add_argument('--no-long-context', action='store_true',
+                    help='skip the Qwen3-8B long-context measurement (8192-token prompt)')
     ap.add_argument('--no-stream', action='store_true', help='skip the streamed generate() measurement')
     ap.add_argument('--no-extra', action='store_true', help='skip the attention and copy measurements')
     ap.add_argument('--dispatch-grid', action='store_true',
@@ -247,17 +258,131 @@ def attention_sweep(lengths=(256, 1024, 4096, 16384)):
     return out
 
 
-def cpu_kernels(threads):
+def launch_floor(chain=64, reps=20):
+    """The fixed cost of one dependent GEMV launch in a graph: `chain` egpt_int8_gemv calls of ONE 2048-wide output
+    row each (2 KB of weights, 16 MB apart in a 1 GiB buffer, so every call's row comes from HBM), each reading the
+    previous call's output. What a call costs beyond its own bytes: the launch boundary, the round trip of its first
+    loads, its reduction and store."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device('cuda')
+    k = 2048
+    w = torch.randint(-127, 128, (1 << 30,), dtype=torch.int8, device=dev)
+    sc = torch.full((1,), 1e-3, device=dev)
+    xs = torch.randn(chain + 1, k, device=dev).to(torch.bfloat16)
+    stride = (1 << 30) // chain
+
+    def run():
+        st = _lib.stream_ptr()
+        for i in range(chain):
+            # the output row is element 0 of the next call's activation row
+            _lib.check('egpt_int8_gemv', lib.egpt_int8_gemv(xs[i].data_ptr(), k, w[i * stride:].data_ptr(), k,
+                                                            sc.data_ptr(), xs[i + 1].data_ptr(), 1, 1, 1, k, st))
+
+    us = _time_graph(run, reps) / chain * 1e6
+    del w
+    torch.cuda.empty_cache()
+    return round(us, 3)
+
+
+CONFIG1_SHAPES = (('qkv', 4096, 2048), ('o_proj', 2048, 2048), ('gate_up', 12288, 2048), ('down', 2048, 6144),
+                  ('lm_head', 151936, 2048))
+
+
+def gemv_small_batch(floor_us, rows=(1, 2, 4, 8), reps=5):
+    """egpt_int8_gemv at each per-layer GEMV shape of Qwen3-1.7B and the lm_head, with M = 1, 2, 4, 8 activation
+    rows, cold (each call streams its own weight copy; the copies of one shape total > 512 MB). Bytes per call are
+    N K + 4 N + 2 M K + 2 M N; `frac_beyond_floor` takes the launch floor out of the time."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device('cuda')
+    out = {}
+    for name, n, k in CONFIG1_SHAPES:
+        sets = max(2, -(-(600 << 20) // (n * k)))
+        g = torch.Generator(device=dev).manual_seed(1)
+        ws = [torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8) for _ in range(sets)]
+        sc = torch.rand(n, generator=g, device=dev) * 1e-3
+        for m in rows:
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+            def run():
+                st = _lib.stream_ptr()
+                for w in ws:
+                    _lib.check('egpt_int8_gemv', lib.egpt_int8_gemv(x.data_ptr(), k, w.data_ptr(), k, sc.data_ptr(),
+                                                                    y.data_ptr(), n, m, n, k, st))
+
+            t = _time_graph(run, reps) / sets
+            nbytes = n * k + 4 * n + 2 * m * k + 2 * m * n
+            gbps = nbytes / t / 1e9
+            beyond = nbytes / max(t - floor_us * 1e-6, 1e-9) / 1e9
+            out[f'{m}x{k}->{n}'] = {'shape': name, 'rows': m, 'us': round(t * 1e6, 2), 'achieved': round(gbps, 1),
+                                   'frac': round(gbps / HBM_PEAK_GBPS, 4),
+                                   'frac_beyond_floor': round(beyond / HBM_PEAK_GBPS, 4)}
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
+def long_context(prompt_len=8192, steps=32, warmup=4, seed=0):
+    """The long-context workload: a random-init Qwen3-8B-architecture int8 model (36 layers, hidden 4096,
+    intermediate 12288, 32 q / 8 kv heads) after a `prompt_len`-token uniform-random prompt, cache of prompt + 512
+    slots; `steps` graph replays timed back to back. The step's GEMV launches are timed on their own
+    (gemv_roofline); the rest of the step, attention and its merge launches plus the argmax, is the step time minus
+    that, over the K/V bytes of the live slots."""
+    from efficientgpt_amd.qwen3 import QWEN3_8B, Qwen3Int8Engine
+    cfg = QWEN3_8B
+    cap = prompt_len + 512
+    eng = Qwen3Int8Engine.random(cfg, cap, seed=seed)
+    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=torch.Generator().manual_seed(seed + 1))
+    with torch.inference_mode():
+        eng.reset()
+        t = time.perf_counter()
+        eng.prefill(prompt)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t
+        eng.capture()
+        for _ in range(warmup):
+            eng.replay()
+        torch.cuda.synchronize()
+        e0, e1 = _events()
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            eng.graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        roof = gemv_roofline(eng)
+    step_ms = wall / steps * 1e3
+    mean_len = prompt_len + warmup + (steps + 1) / 2
+    kv_bytes = cfg.kv_bytes_per_slot() * mean_len
+    rest_ms = step_ms - roof['gemv_ms_per_step']
+    wbytes, sbytes = cfg.weight_bytes()
+    step_bytes = wbytes + sbytes + kv_bytes
+    nsplit = eng.nsplit
+    del eng
+    torch.cuda.empty_cache()
+    return {'workload': f'qwen3-8b int8, {prompt_len}-token prompt, cache {cap} slots, {steps} graph replays',
+            'value': round(steps / wall, 2), 'unit': 'tok/s', 'ms_per_step': round(step_ms, 4),
+            'prefill_s': round(prefill_s, 3), 'mean_kv_len': mean_len, 'nsplit': nsplit,
+            'step_frac': round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            'gemv': {k: roof[k] for k in ('achieved', 'frac', 'launches', 'avg_launch_us', 'gemv_ms_per_step')},
+            'attention_and_rest': {'ms_per_step': round(rest_ms, 4), 'kv_bytes': int(kv_bytes),
+                                   'achieved': round(kv_bytes / (rest_ms * 1e-3) / 1e9, 1),
+                                   'frac': round(kv_bytes / (rest_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
+
+
+def cpu_kernels(threads, rows=(1, 2, 4, 8), lengths=(256, 1024, 4096, 16384, 32768)):
     """The reference's CPU-runnable forms of the two kernels on this host, beside the GPU figures:
-    the int8 linear's formula ((x @ W.bf16^T).float() * s).bf16 (research/realmodel/int8_linear.py:97)
-    at 1 x 2048 -> 6144, median of 20 calls; fp32 SDPA over 32768 slots, 16 q / 8 kv heads (the kv
-    heads repeated per group), median of 5 calls. Bytes are the kernels' algorithmic bytes."""
+    - the int8 linear's formula ((x @ W.bf16^T).float() * s).bf16 (research/realmodel/int8_linear.py:97) at every
+      per-layer GEMV shape of Qwen3-1.7B and the lm_head, M = 1, 2, 4, 8 rows, median of 20 calls; the exact bf16
+      image of W is built once per shape and reused (numerically identical to converting per call);
+    - fp32 SDPA of one query per head over L slots, 16 q / 8 kv heads of 128 (the kv heads repeated per group),
+      median of 5 calls, at L = 256 ... 32768.
+    Bytes are the kernels' algorithmic bytes (N K + 4 N + 2 M K + 2 M N; 4096 L + 8192)."""
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
-    n, k = 6144, 2048
-    x = torch.randn(1, k, generator=g).to(torch.bfloat16)
-    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
-    sc = torch.randn(n, generator=g).abs() * 0.02 / 127
 
     def timed(fn, reps):
         fn()
@@ -268,17 +393,28 @@ def cpu_kernels(threads):
             ts.append(time.perf_counter() - t)
         return sorted(ts)[len(ts) // 2]
 
-    t_gemv = timed(lambda: ((x @ w.to(torch.bfloat16).t()).float() * sc).to(torch.bfloat16), 20)
-    hq, hkv, L, d = 16, 8, 32768, 128
-    q = torch.randn(1, hq, 1, d, generator=g)
-    kv = torch.randn(2, 1, hkv, L, d, generator=g).to(torch.bfloat16).float()
-    kk, vv = kv[0].repeat_interleave(hq // hkv, 1), kv[1].repeat_interleave(hq // hkv, 1)
-    t_attn = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, kk, vv), 5)
-    gb = n * k + 4 * n + 2 * k + 2 * n
-    ab = 2 * hkv * L * d * 2 + 2 * (2 * hq * d)
-    return {'gemv_1x2048_6144': {'us': round(t_gemv * 1e6, 1), 'achieved_gbps': round(gb / t_gemv / 1e9, 2)},
-            'attention_L32768': {'us': round(t_attn * 1e6, 1), 'achieved_gbps': round(ab / t_attn / 1e9, 2)},
-            'threads': threads}
+    gemv = {}
+    for name, n, k in CONFIG1_SHAPES:
+        w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+        wb = w.to(torch.bfloat16)
+        sc = torch.randn(n, generator=g).abs() * 0.02 / 127
+        for m in rows:
+            x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+            t = timed(lambda: ((x @ wb.t()).float() * sc).to(torch.bfloat16), 20)
+            nbytes = n * k + 4 * n + 2 * m * k + 2 * m * n
+            gemv[f'{m}x{k}->{n}'] = {'shape': name, 'rows': m, 'us': round(t * 1e6, 1),
+                                     'achieved_gbps': round(nbytes / t / 1e9, 2)}
+        del w, wb
+    attn = {}
+    hq, hkv, d = 16, 8, 128
+    for L in lengths:
+        q = torch.randn(1, hq, 1, d, generator=g)
+        kv = torch.randn(2, 1, hkv, L, d, generator=g).to(torch.bfloat16).float()
+        kk, vv = kv[0].repeat_interleave(hq // hkv, 1), kv[1].repeat_interleave(hq // hkv, 1)
+        t = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, kk, vv), 5)
+        attn[str(L)] = {'us': round(t * 1e6, 1), 'achieved_gbps': round((4096 * L + 8192) / t / 1e9, 2)}
+    return {'gemv': gemv, 'attention': attn, 'threads': threads,
+            'gemv_note': 'bf16 image of the int8 weights built once per shape, then x @ W^T, fp32 scale, bf16'}
 
 
 def copy_bandwidth(nbytes=1 << 30, reps=10):
@@ -314,13 +450,17 @@ def near_tie_bound(top1):
 
 
 def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
-    """The CPU oracle on the same weights: prefill the prompt, then n_tokens greedy steps."""
+    """The CPU oracle on the same weights: prefill the prompt, then greedy tokens until n_tokens are out.
+    Decode tok/s = (n - 1) / (total - TTFT), the reference's client-side rule (assistant/backends.py:276,
+    research/realmodel/bench_int8.py)."""
     from oracle.qwen3 import Qwen3Oracle, Qwen3Shape
     c = eng.cfg
     torch.set_num_threads(host_threads())
     shape = Qwen3Shape(c.vocab, c.hidden, c.inter, c.layers, c.heads, c.kv_heads, c.head_dim, c.rope_theta,
                        c.rms_eps, c.tied)
     orc = Qwen3Oracle(shape, eng.weights, dtype=torch.bfloat16, cap=len(prompt) + n_tokens + 1)
+    orc.forward(prompt[:1], 0)  # builds the cached fp32 images of the int8 weights outside the timed run
+    orc.reset()
     margins = []  # (top-1 - top-2, top-1) of the oracle's logits at each step
 
     def pick(logits):
@@ -347,9 +487,11 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
                  f'against the near-tie bound {bound:.4g} ({"a near-tie" if m < bound else "NOT a near-tie"})')
     return {'value': round(decode_tps, 3) if decode_tps else None, 'unit': 'tok/s', 'cores': torch.get_num_threads(),
             'kind': 'port',
-            'sample': (f'CPU oracle (torch, bf16 activations, exact fp32 image of the int8 weights) on the same '
-                       f'weights: prefill of the {len(prompt)}-token prompt ({t_first - t0:.1f} s), then '
-                       f'{n_tokens} greedy tokens; decode tok/s = (n-1)/(decode time)'),
+            'sample': (f'CPU oracle (torch, bf16 activations, exact fp32 image of the int8 weights built before '
+                       f'timing) on the same weights and prompt: prefill of the {len(prompt)}-token prompt (TTFT '
+                       f'{t_first - t0:.2f} s), then {n_tokens} greedy tokens in {t1 - t0:.1f} s; decode tok/s = '
+                       f'(n-1)/(total-TTFT)'),
+            'ttft_s': round(t_first - t0, 3), 'total_s': round(t1 - t0, 3), 'tokens': n_tokens,
             'cpu': platform.processor() or platform.machine(),
             'token_agreement_with_gpu': agree}
 
@@ -442,11 +584,24 @@ def main():
     extra = {}
     if not args.no_extra:
         with torch.inference_mode():  # graph capture after the engine's inference-mode captures
+            floor = launch_floor()
+            extra['launch_floor_us'] = floor
             extra['attention'] = attention_roofline()
             extra['attention_by_length'] = attention_sweep()
             extra['gemv_1x2048_6144'] = gemv_cfg0()
+            # each small kernel's own share: its bytes over its time less the launch floor (one per launch)
+            g0 = extra['gemv_1x2048_6144']
+            g0['frac_beyond_floor'] = round(g0['bytes_per_call'] / max(g0['us_per_call'] - floor, 1e-3) / 1e3
+                                            / HBM_PEAK_GBPS, 4)
+            for L, r in list(extra['attention_by_length'].items()) + [('32768', extra['attention'])]:
+                launches = 1 if r['nsplit'] == 1 else 2  # the split kernel, then the combine
+                r['frac_beyond_floor'] = round((4096 * int(L) + 8192) / max(r['us_per_call'] - launches * floor, 1e-3)
+                                               / 1e3 / HBM_PEAK_GBPS, 4)
+            extra['gemv_small_batch'] = gemv_small_batch(floor)
             extra['prefill_gemm'] = prefill_gemm()
             extra['copy_gbps'] = copy_bandwidth()
+    if args.model == 'qwen3-1.7b' and not args.no_long_context:
+        extra['long_context'] = long_context()
     cpu = None
     if args.cpu_tokens > 0 and gpu_tokens and args.model == 'qwen3-1.7b':
         cpu = cpu_baseline(eng, prompt, args.cpu_tokens, gpu_tokens)
