@@ -212,9 +212,9 @@ def gemv_cfg0(n=6144, k=2048, sets=48, reps=10):
                       'weight copy, each call including its hand-off from the previous launch'}
 
 
-def prefill_gemm(rows=(128, 1024), shapes=((4096, 2048), (12288, 2048), (2048, 6144)), reps=3):
-    """The prefill GEMM (egpt_int8_gemm, bf16 MFMA on int8 weights) at Qwen3-1.7B's QKV, gate/up and down
-    shapes, beside the reference's formula for the same product (research/realmodel/int8_linear.py:96-97:
+def prefill_gemm(rows=(128, 1024), shapes=((4096, 2048), (12288, 2048), (2048, 6144), (2048, 2048)), reps=3):
+    """The prefill GEMM (egpt_int8_gemm_ws, bf16 MFMA on int8 weights, K split over a workspace where the output
+    tiles alone leave CUs idle) at Qwen3-1.7B's QKV, gate/up, down and o_proj shapes, beside the reference's formula for the same product (research/realmodel/int8_linear.py:96-97:
     dequantise to bf16, library GEMM, scale). TF/s of 2 M N K flops; peak dense bf16 MFMA 2500 TF/s."""
     from efficientgpt_amd import _lib
     lib = _lib.lib()
@@ -228,11 +228,15 @@ def prefill_gemm(rows=(128, 1024), shapes=((4096, 2048), (12288, 2048), (2048, 6
             sc = torch.rand(n, generator=g, device=dev) * 1e-3
             y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
             calls = max(1, int(2e11 // (2 * m * n * k)))
+            need = ctypes.c_size_t()
+            _lib.check('egpt_int8_gemm_workspace', lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(need)))
+            ws = torch.empty(max(need.value, 16), device=dev, dtype=torch.uint8)
 
             def ours():
                 for _ in range(calls):
-                    _lib.check('egpt_int8_gemm', lib.egpt_int8_gemm(x.data_ptr(), k, q.data_ptr(), k, sc.data_ptr(),
-                                                                    y.data_ptr(), n, m, n, k, _lib.stream_ptr()))
+                    _lib.check('egpt_int8_gemm_ws', lib.egpt_int8_gemm_ws(
+                        x.data_ptr(), k, q.data_ptr(), k, sc.data_ptr(), y.data_ptr(), n, m, n, k, ws.data_ptr(),
+                        need.value, _lib.stream_ptr()))
 
             def reference():
                 for _ in range(calls):
@@ -241,7 +245,7 @@ def prefill_gemm(rows=(128, 1024), shapes=((4096, 2048), (12288, 2048), (2048, 6
             t_ours = _time_graph(ours, reps) / calls
             t_ref = _time_graph(reference, reps) / calls
             fl = 2 * m * n * k
-            out.append({'shape': f'{m}x{k} -> {n}', 'us': round(t_ours * 1e6, 1),
+            out.append({'shape': f'{m}x{k} -> {n}', 'us': round(t_ours * 1e6, 1), 'k_splits': need.value // (m * n * 4),
                         'tflops': round(fl / t_ours / 1e12, 1), 'frac': round(fl / t_ours / 2.5e15, 4),
                         'reference_formula_us': round(t_ref * 1e6, 1)})
             del x, q, y

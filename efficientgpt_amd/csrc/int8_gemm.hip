@@ -22,9 +22,16 @@
 //     padding puts the fragment reads of 16 consecutive rows on distinct banks.
 //   * int8 -> bf16 is exact: every value in [-127, 127] is a bf16.
 //   * Rows past M or N read a valid row and are never stored.
+//   * Split-K (short M, long K: too few output tiles to give every CU a block):
+//     block (split, tile) sums its K slice and stores the fp32 tile to a caller's
+//     workspace [splits][M][N]; a second kernel adds the slices in split order and
+//     applies the two roundings. The fp32 sum is the same product in another
+//     order, as any GEMM blocking is.
 // Operand layouts (checked on the MI355X): lane l holds A[l % 32][8 (l / 32) + e]
 // and B[8 (l / 32) + e][l % 32], e = 0..7; accumulator register r of lane l is
 // C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+#include <algorithm>
+
 #include "common.h"
 
 namespace egpt {
@@ -34,16 +41,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmThreads = 256;
-constexpr int kBK = 64;               // K per LDS stage
-constexpr int kLdsRow = kBK + 8;      // bf16 elements per x row in LDS (16 bytes of padding)
-constexpr int kLdsRowW = kBK + 16;    // bytes per int8 weight row in LDS (16 bytes of padding)
+constexpr int kBK = 64;        // K per LDS stage of the one-pass kernel: K must be a multiple of it
+constexpr int kBKSplit = 128;  // K per LDS stage of the split-K slices (half the dependent steps)
 
-template <int BM, int BN>
+template <int BM, int BN, int BK>
 struct GemmShape {
   static constexpr int TM = BM / 64;  // 32 x 32 tiles per wavefront along M
   static constexpr int TN = BN / 64;  // ... along N
-  static constexpr int kALoads = BM * kBK * 2 / (kGemmThreads * 16);  // 16-byte x loads per thread per step
-  static constexpr int kBLoads = BN * kBK / (kGemmThreads * 16);      // 16-byte int8 loads per thread per step
+  static constexpr int kLdsRow = BK + 8;    // bf16 elements per x row in LDS (16 bytes of padding)
+  static constexpr int kLdsRowW = BK + 16;  // bytes per int8 weight row in LDS (16 bytes of padding)
+  static constexpr int kALoads = BM * BK * 2 / (kGemmThreads * 16);  // 16-byte x loads per thread per step
+  static constexpr int kBLoads = BN * BK / (kGemmThreads * 16);      // 16-byte int8 loads per thread per step
   static_assert(TM >= 1 && TN >= 1 && kALoads >= 1 && kBLoads >= 1, "tile too small for the block");
 };
 
@@ -73,6 +81,8 @@ struct GemmArgs {
   int64_t ldy;
   int M, N, K;
   int tiles_m, tiles_n;
+  int splits, kchunk;  // K slices (1: no split) of kchunk columns each, the last one shorter
+  float* part;         // splits > 1: fp32 partial tiles [splits][M][N]
 };
 
 constexpr int kXcds = 8;        // MI355X: 8 XCDs, each with its own L2
@@ -97,10 +107,11 @@ __device__ __forceinline__ void gemm_tile(int b, int tiles_m, int tiles_n, int& 
   pid_n = (t % group) / gm;
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int BK, bool SPLIT>
 __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs a) {
-  using S = GemmShape<BM, BN>;
+  using S = GemmShape<BM, BN, BK>;
   constexpr int TM = S::TM, TN = S::TN;
+  constexpr int kLdsRow = S::kLdsRow, kLdsRowW = S::kLdsRowW;
   __shared__ __align__(16) uint16_t As[2][BM * kLdsRow];
   __shared__ __align__(16) int8_t Bs[2][BN * kLdsRowW];
 
@@ -109,10 +120,13 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   const int wave = tid / kWave;
   const int wm0 = (wave / 2) * (BM / 2);  // wavefront tile origin in the block tile
   const int wn0 = (wave % 2) * (BN / 2);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int split = SPLIT ? (int)blockIdx.x / tiles : 0;
   int pid_m, pid_n;
-  gemm_tile(blockIdx.x, a.tiles_m, a.tiles_n, pid_m, pid_n);
+  gemm_tile((int)blockIdx.x - split * tiles, a.tiles_m, a.tiles_n, pid_m, pid_n);
   const int64_t m0 = (int64_t)pid_m * BM;
   const int64_t n0 = (int64_t)pid_n * BN;
+  const int kbeg = SPLIT ? split * a.kchunk : 0;  // this block's K slice [kbeg, kbeg + nk * BK)
 
   // global -> register staging of one K step
   const uint16_t* xsrc[S::kALoads];
@@ -120,8 +134,8 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
 #pragma unroll
   for (int j = 0; j < S::kALoads; ++j) {
     const int i = tid + j * kGemmThreads;
-    const int row = i / (kBK / 8), chunk = i % (kBK / 8);
-    xsrc[j] = a.x + min(m0 + row, (int64_t)a.M - 1) * a.ldx + chunk * 8;
+    const int row = i / (BK / 8), chunk = i % (BK / 8);
+    xsrc[j] = a.x + min(m0 + row, (int64_t)a.M - 1) * a.ldx + kbeg + chunk * 8;
     a_lds[j] = row * kLdsRow + chunk * 8;
   }
   const int8_t* wsrc[S::kBLoads];
@@ -129,18 +143,18 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
 #pragma unroll
   for (int j = 0; j < S::kBLoads; ++j) {
     const int i = tid + j * kGemmThreads;
-    const int row = i / (kBK / 16), chunk = i % (kBK / 16);
-    wsrc[j] = a.w + min(n0 + row, (int64_t)a.N - 1) * a.ldw + chunk * 16;
+    const int row = i / (BK / 16), chunk = i % (BK / 16);
+    wsrc[j] = a.w + min(n0 + row, (int64_t)a.N - 1) * a.ldw + kbeg + chunk * 16;
     b_lds[j] = row * kLdsRowW + chunk * 16;
   }
   // Two register staging sets: the loads of step k + 2 are issued while step k is
   // multiplied and land in LDS at the end of step k + 1, about two steps of MFMA
   // work later. Loads past the last step re-read the last K slice (in bounds, never
   // stored), so every load is unconditional and each wait is for one set only.
-  const int nk = a.K / kBK;
+  const int nk = (SPLIT ? min(a.kchunk, a.K - kbeg) : a.K) / BK;
   u32x4 xr[2][S::kALoads], wr[2][S::kBLoads];
   auto load_step = [&](int kt, int set) {
-    const int k0 = min(kt, nk - 1) * kBK;
+    const int k0 = min(kt, nk - 1) * BK;
 #pragma unroll
     for (int j = 0; j < S::kALoads; ++j) xr[set][j] = ld16(xsrc[j] + k0);
 #pragma unroll
@@ -170,7 +184,7 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   // The MFMAs of one K step from LDS buffer `buf`, 16 K columns at a time.
   auto mma_step = [&](int buf) {
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
+    for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 af[TM], bfr[TN];
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm) af[tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
@@ -215,6 +229,21 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   }
   if (kt < nk) mma_step(0);
 
+  if constexpr (SPLIT) {  // the fp32 tile of this K slice; the reduce kernel rounds
+    float* part = a.part + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int64_t n = n0 + wn0 + tn * 32 + lane % 32;
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = m0 + wm0 + tm * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+          if (m < a.M && n < a.N) part[m * a.N + n] = acc[tm][tn][r];
+        }
+    }
+    return;
+  }
   // y = bf16(bf16(acc) * scale): the reference's two roundings
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
@@ -234,6 +263,23 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   }
 }
 
+// Split-K reduce: y[m, n] = bf16(bf16(sum_s part[s][m][n]) * scale[n]), splits added in order.
+constexpr int kReduceThreads = 256;
+
+__global__ __launch_bounds__(kReduceThreads) void int8_gemm_reduce_kernel(const float* __restrict__ part,
+                                                                          const float* __restrict__ scale,
+                                                                          uint16_t* __restrict__ y, int64_t ldy, int M,
+                                                                          int N, int splits) {
+  const int64_t mn = (int64_t)M * N;
+  for (int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x; i < mn;
+       i += (int64_t)gridDim.x * kReduceThreads) {
+    float acc = part[i];
+    for (int sp = 1; sp < splits; ++sp) acc += part[sp * mn + i];
+    const int64_t m = i / N, n = i - m * N;
+    y[m * ldy + n] = f32_to_bf16(bf16_to_f32(f32_to_bf16(acc)) * scale[n]);
+  }
+}
+
 template <int BM, int BN>
 unsigned gemm_blocks(const GemmArgs& a) {
   return (unsigned)(((int64_t)a.N + BN - 1) / BN) * (unsigned)(((int64_t)a.M + BM - 1) / BM);
@@ -243,9 +289,40 @@ template <int BM, int BN>
 int launch_gemm(GemmArgs a, hipStream_t st) {
   a.tiles_m = (int)(((int64_t)a.M + BM - 1) / BM);
   a.tiles_n = (int)(((int64_t)a.N + BN - 1) / BN);
-  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN>), dim3((unsigned)a.tiles_m * (unsigned)a.tiles_n),
-                     dim3(kGemmThreads), 0, st, a);
+  const unsigned tiles = (unsigned)a.tiles_m * (unsigned)a.tiles_n;
+  if constexpr (BM == 64 && BN == 64) {  // split-K runs 64 x 64 tiles
+    if (a.splits > 1) {
+      hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBKSplit, true>), dim3(tiles * (unsigned)a.splits),
+                         dim3(kGemmThreads), 0, st, a);
+      if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
+      const int64_t mn = (int64_t)a.M * a.N;
+      const unsigned blocks = (unsigned)std::min<int64_t>((mn + kReduceThreads - 1) / kReduceThreads, 4096);
+      hipLaunchKernelGGL(int8_gemm_reduce_kernel, dim3(blocks), dim3(kReduceThreads), 0, st, a.part, a.scale, a.y,
+                         a.ldy, a.M, a.N, a.splits);
+      return EGPT_LAUNCH_STATUS();
+    }
+  }
+  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false>), dim3(tiles), dim3(kGemmThreads), 0, st, a);
   return EGPT_LAUNCH_STATUS();
+}
+
+// K slices for a short-M GEMM whose 64 x 64 tiles leave CUs idle: the fewest
+// (a power of two, at most 16) that give every CU a block, each slice a multiple
+// of kBKSplit and at least 256 wide. 1 when the tiles already fill the chip, or K
+// is short or not a multiple of kBKSplit.
+constexpr int kMinSliceSteps = 4;
+constexpr int kMaxSplits = 16;
+constexpr int kSplitTargetBlocks = 256;
+
+void gemm_split(int64_t M, int64_t N, int64_t K, int& splits, int& kchunk) {
+  const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  splits = 1;
+  kchunk = (int)K;
+  if (M > 128 || K % kBKSplit) return;  // taller blocks take the larger tiles below
+  while (tiles * splits < kSplitTargetBlocks && splits < kMaxSplits && K / (2 * splits) >= kMinSliceSteps * kBK) splits *= 2;
+  if (splits == 1) return;
+  kchunk = (int)(((K + splits - 1) / splits + kBKSplit - 1) / kBKSplit * kBKSplit);
+  splits = (int)((K + kchunk - 1) / kchunk);
 }
 
 }  // namespace
@@ -253,19 +330,45 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
 
 using namespace egpt;
 
-extern "C" int egpt_int8_gemm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y,
-                              int64_t ldy, int M, int N, int K, hipStream_t stream) {
+extern "C" int egpt_int8_gemm_workspace(int M, int N, int K, size_t* bytes) {
+  if (!bytes || M < 0 || N < 0 || K < 0) return EGPT_ERR_INVALID;
+  int splits, kchunk;
+  gemm_split(M, N, K, splits, kchunk);
+  *bytes = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+  return EGPT_OK;
+}
+
+extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale,
+                                 void* y, int64_t ldy, int M, int N, int K, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
   if (!x || !w || !scale || !y || M < 0 || N < 0 || K < 0) return EGPT_ERR_INVALID;
   if (ldx < K || ldw < K || ldy < N) return EGPT_ERR_INVALID;
   if (M == 0 || N == 0) return EGPT_OK;
   if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
     return EGPT_ERR_UNSUPPORTED;
-  if (((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX) return EGPT_ERR_UNSUPPORTED;
-  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0};
+  if (((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX / kMaxSplits) return EGPT_ERR_UNSUPPORTED;
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0, 1, K, nullptr};
+  if (workspace) {  // a workspace lets short-M shapes split K
+    int splits, kchunk;
+    gemm_split(M, N, K, splits, kchunk);
+    if (splits > 1) {
+      if (workspace_bytes < (size_t)splits * (size_t)M * (size_t)N * sizeof(float) || (uintptr_t)workspace % 16)
+        return EGPT_ERR_WORKSPACE;
+      a.splits = splits;
+      a.kchunk = kchunk;
+      a.part = (float*)workspace;
+      return launch_gemm<64, 64>(a, stream);
+    }
+  }
   // The largest tile that still gives every CU a block; small M keeps more, narrower tiles.
   if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm<256, 256>(a, stream);
   if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256>(a, stream);
   if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128>(a, stream);
   if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
   return launch_gemm<64, 64>(a, stream);
+}
+
+extern "C" int egpt_int8_gemm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y,
+                              int64_t ldy, int M, int N, int K, hipStream_t stream) {
+  return egpt_int8_gemm_ws(x, ldx, w, ldw, scale, y, ldy, M, N, K, nullptr, 0, stream);
 }

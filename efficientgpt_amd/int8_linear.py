@@ -115,8 +115,13 @@ def int8_gemm(x2, w, s, out=None):
     if m > GEMM_KERNEL_MAX_ROWS:
         out.copy_(((x2 @ w.to(torch.bfloat16).t()).float() * s).to(torch.bfloat16))
         return out
-    st = _lib.lib().egpt_int8_gemm(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), s.data_ptr(),
-                                   out.data_ptr(), out.stride(0), m, n, k, _lib.stream_ptr(x2.device))
+    lib = _lib.lib()
+    need = ctypes.c_size_t()
+    _lib.check('egpt_int8_gemm_workspace', lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(need)))
+    ws = torch.empty(need.value, device=x2.device, dtype=torch.uint8) if need.value else None
+    st = lib.egpt_int8_gemm_ws(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), s.data_ptr(),
+                               out.data_ptr(), out.stride(0), m, n, k, ws.data_ptr() if ws is not None else None,
+                               need.value, _lib.stream_ptr(x2.device))
     if st == _lib.EGPT_ERR_UNSUPPORTED:
         out.copy_(((x2 @ w.to(torch.bfloat16).t()).float() * s).to(torch.bfloat16))
     else:

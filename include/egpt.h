@@ -77,6 +77,18 @@ int egpt_int8_gemv_splitk(const void *x, int64_t ldx, const int8_t *w, int64_t l
  */
 int egpt_int8_gemm(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                    void *y, int64_t ldy, int M, int N, int K, hipStream_t stream);
+/* The same product with a workspace, which lets short-M shapes (M <= 128 whose
+ * 64 x 64 output tiles leave CUs idle) split K: each split's fp32 tile goes to the
+ * workspace and a second launch adds the splits in order, then rounds as above.
+ * egpt_int8_gemm_workspace gives the bytes the split needs for this shape (0: no
+ * split; the workspace may then be NULL). Same result contract as egpt_int8_gemm
+ * (the fp32 sum in another order). Replaces the same reference formula
+ * (research/realmodel/int8_linear.py:96-97); the split mirrors the reference's
+ * split-K GEMV (:41-64) for the GEMM. */
+int egpt_int8_gemm_workspace(int M, int N, int K, size_t *bytes);
+int egpt_int8_gemm_ws(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                      void *y, int64_t ldy, int M, int N, int K, void *workspace, size_t workspace_bytes,
+                      hipStream_t stream);
 
 /*
  * Split-K GQA decode attention (flash decoding) with its partial-softmax reduce.

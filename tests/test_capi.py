@@ -106,3 +106,15 @@ def test_struct_layouts_match_the_header(tmp_path):
     want = [ctypes.sizeof(_lib.GemvFused), _lib.GemvFused.part_i.offset, _lib.GemvFused.w.offset,
             ctypes.sizeof(_lib.Qwen3Step), _lib.Qwen3Step.workspace_bytes.offset, ctypes.sizeof(_lib.Qwen3Layer)]
     assert got == want
+
+
+def test_gemm_split_workspace_policy():
+    """Short-M prefill shapes split K until every CU has a block (at most 16 splits, at least 4 K steps of 64
+    each); tall ones and short K do not split."""
+    lib = _lib.lib()
+    size = ctypes.c_size_t()
+    for (m, n, k), splits in (((128, 2048, 6144), 4), ((128, 4096, 2048), 2), ((64, 2048, 2048), 8),
+                              ((17, 64, 12288), 16), ((128, 12288, 2048), 0), ((1024, 2048, 6144), 0),
+                              ((128, 2048, 256), 0)):
+        assert lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(size)) == 0
+        assert size.value == splits * m * n * 4, (m, n, k, size.value)

@@ -229,6 +229,41 @@ def test_prefill_gemm_kernel_matches_oracle(m, k, n):
     assert float((diff == 0).float().mean()) >= 0.9
 
 
+SPLIT_SHAPES = [(128, 6144, 2048), (128, 2048, 4096), (33, 6144, 2048), (64, 2048, 2048), (100, 4096, 1000),
+                (17, 12288, 64)]
+
+
+@pytest.mark.parametrize('m,k,n', SPLIT_SHAPES)
+def test_prefill_gemm_split_k_matches_oracle(m, k, n):
+    """Short-M shapes whose 64 x 64 tiles leave CUs idle split K through a workspace (egpt_int8_gemm_ws): the
+    splits' fp32 tiles are added in order, then rounded as the reference's formula. Same bounds as the one-pass
+    kernel, and the same result as it on all but the elements whose fp32 sum rounds differently."""
+    from efficientgpt_amd import _lib
+    import ctypes
+    lib = _lib.lib()
+    need = ctypes.c_size_t()
+    assert lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(need)) == 0
+    assert need.value > 0 and need.value % (m * n * 4) == 0, need.value
+    x, q, s = make_case(m, k, n, seed=m + k + n)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    ws = torch.empty(need.value, device='cuda', dtype=torch.uint8)
+    y = torch.empty(m, n, device='cuda', dtype=torch.bfloat16)
+    st = lib.egpt_int8_gemm_ws(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), y.data_ptr(), n, m, n, k,
+                               ws.data_ptr(), need.value, _lib.stream_ptr())
+    assert st == 0, st
+    check_against_oracle(y.cpu(), x, q, s)
+    one = torch.empty_like(y)
+    assert lib.egpt_int8_gemm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), one.data_ptr(), n, m, n, k,
+                              _lib.stream_ptr()) == 0
+    assert float((one == y).float().mean()) >= 0.9
+    # too small a workspace is refused before any launch
+    assert lib.egpt_int8_gemm_ws(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), y.data_ptr(), n, m, n, k,
+                                 ws.data_ptr(), need.value - 4, _lib.stream_ptr()) == -4
+    # the op takes the split path and reproduces it bit for bit
+    from efficientgpt_amd.int8_linear import int8_linear
+    assert torch.equal(int8_linear(xd, qd, sd), y)
+
+
 def test_prefill_op_uses_kernel_and_falls_back_for_unaligned_k():
     from efficientgpt_amd import _lib
     from efficientgpt_amd.int8_linear import int8_linear
