@@ -379,6 +379,277 @@ __device__ __forceinline__ void attn_partial(const float (&qf)[G][Geo::EPL], Att
   }
 }
 
+// ---------------------------------------------------------------- q . k on MFMA
+//
+// The whole-group form for bf16 caches, D = 128 and G = 4 query heads per kv head
+// (attn_partial_mfma; written for G = 2 too, see kAttnMfma). A wavefront runs ONE softmax stream over tiles of 16
+// slots, wavefront w of the block taking tiles w, w + 4, ... of the split:
+//   * scores: S[16 slots x 16 cols] = K[16 x 128] . Q^T[128 x 16] by four
+//     v_mfma_f32_16x16x32_bf16 (bf16 products exact, fp32 sums), query heads in
+//     columns 0..G-1. K goes straight from memory into the A operand: lane l
+//     loads 16 bytes of slot l % 16 at dims 32 c + 8 (l / 16), so a tile is four
+//     16-byte loads per lane and every byte is read once. Lane l then holds the
+//     scores of head l % 16 for slots 4 (l / 16) + r, r = 0..3.
+//   * softmax: per head over the tile's 16 slots (own 4, then the lanes l ^ 16 and
+//     l ^ 32), the online update in fp32 as in attn_mac; each lane keeps (m, l) of
+//     head l % 16.
+//   * p . v stays in fp32 FMAs (the reference's tl.sum(p * v)): the tile's p go
+//     to a 16 x 16 LDS tile of the wavefront, and lane l, holding 8 dims
+//     8 (l % 16) .. of V rows 4 t + l / 16 (t = 0..3, the row layout of
+//     attn_issue), reads p of its row for the G heads. acc then sums a quarter of
+//     the slots per lane group, all under the stream's one max, so the four groups
+//     are added at the end with no rescaling.
+// Per 16 slots this is 4 MFMAs and about 8 G + 70 VALU instructions per
+// wavefront, against about 33 per slot for the vector form at G = 4 (16-lane
+// reductions of every q . k). The four streams of a block merge as in attn_partial.
+typedef __bf16 bf16x8_mt __attribute__((ext_vector_type(8)));
+typedef float f32x4_mt __attribute__((ext_vector_type(4)));
+
+// Whether a block of G query heads over D-element rows of T takes the MFMA form:
+// at 4 query heads per kv head (Qwen3-8B's 32 / 8). Measured on the MI355X against
+// the vector form, cold: stand-alone attention at 32 / 8 heads 32.4 -> 28.8 us at
+// L = 32768 and 21.0 -> 18.3 us at 16384; the Qwen3-8B step after an 8192-token
+// prompt 457 -> 471 tok/s. At 2 heads per kv head (16 / 8) the vector form's
+// arithmetic is not what bounds it: the MFMA form was within noise at 4096-32768
+// slots (27.4 against 28.1 us at 32768) and slower at 256 (6.5 against 5.7 us), and
+// the Qwen3-1.7B step at a 3500-token prompt 0.4% slower; G = 2 keeps the vector form.
+template <typename T, int D, int G>
+constexpr bool kAttnMfma = __is_same(T, __bf16) && D == 128 && G == 4;
+
+constexpr int kMfmaSlots = 16;  // slots of one wavefront tile
+
+struct MfmaKV {
+  u32x4 k[4];  // A operand: 16 slots x 32 dims per chunk
+  u32x4 v[4];  // row layout: slot 4 t + l / 16, dims 8 (l % 16) ..
+};
+
+// Loads of the tile [n0, n0 + 16) of a wavefront. Slots at or past `end` read
+// slot 0 instead (in bounds and live for any position) and are masked out of the
+// softmax, so every load is unconditional and the wait counts stay exact.
+__device__ __forceinline__ void mfma_issue(MfmaKV& t, const __bf16* __restrict__ kb, int64_t k_sn,
+                                           const __bf16* __restrict__ vb, int64_t v_sn, int64_t n0, int64_t end) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t nk = n0 + (lane & 15);
+  const __bf16* kr = kb + (nk < end ? nk : 0) * k_sn + 8 * (lane >> 4);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) t.k[c] = ld16_stream(kr + 32 * c);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t nv = n0 + 4 * r + (lane >> 4);
+    t.v[r] = ld16_stream(vb + (nv < end ? nv : 0) * v_sn + 8 * (lane & 15));
+  }
+}
+
+// One tile of a wavefront's stream: qb are the B fragments of Q^T (4 chunks of 32
+// dims), (m, l) the state of head lane % 16, acc[g][e] the row-layout sums of head
+// g at dim 8 (lane % 16) + e, lds_p the wavefront's 16 x 16 p tile.
+template <int G>
+__device__ __forceinline__ void mfma_mac(const MfmaKV& t, const bf16x8_mt (&qb)[4], int64_t n0, int64_t end,
+                                         float scale, float& m, float& l, float (&acc)[G][8], float* lds_p) {
+  const int lane = threadIdx.x % kWave;
+  f32x4_mt sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_mt, t.k[c]), qb[c], sc, 0, 0, 0);
+  float sv[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t slot = n0 + 4 * (lane >> 4) + r;
+    sv[r] = slot < end ? sc[r] * scale : -INFINITY;  // the reference's fp32 logit: (q . k) * scale
+    mx = fmaxf(mx, sv[r]);
+  }
+  LanePair pr = pair16(mx);
+  mx = fmaxf(pr.lo, pr.hi);
+  pr = pair32(mx);
+  mx = fmaxf(pr.lo, pr.hi);
+  const float mt = fmaxf(m, mx);
+  const float mref = mt == -INFINITY ? 0.f : mt;  // no valid slot yet: the state stays (-inf, 0, 0)
+  const float alpha = exp2_softmax((m - mref) * kLog2e);
+  float ps = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float p = exp2_softmax((sv[r] - mref) * kLog2e);  // 0 for masked slots
+    ps += p;
+    lds_p[(4 * (lane >> 4) + r) * 16 + (lane & 15)] = p;
+  }
+  pr = pair16(ps);
+  ps = pr.lo + pr.hi;
+  pr = pair32(ps);
+  ps = pr.lo + pr.hi;
+  l = l * alpha + ps;
+  m = mt;
+  // the p tile is read back across lanes of this wavefront only
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float ag = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float vf[8];
+    Elem<__bf16>::unpack(t.v[r], vf);
+    const float* prow = lds_p + (4 * r + (lane >> 4)) * 16;
+    float pg[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) pg[g] = prow[g];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
+  }
+  // the next tile's p must not overwrite this one before every lane has read it
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// The whole-group partial state over slots [start, end) for G query heads, a
+// stream per wavefront (see above), continuing from the first tile `t0` that the
+// caller issued at start + 16 * wave. qb: this lane's B fragments of Q^T (column
+// lane % 16 is query head lane % 16 of the group; zero past G). If xnew is set,
+// the new token (key xk, value xv: this lane's 8 dims 8 (lane % 16) .., fp32;
+// qf: this lane's 8 dims of every query head) starts wavefront 0's stream. Output
+// as attn_partial: partials at `row`, or `out` when one split covers every slot.
+// Must be called by all kAttnThreads threads of the block.
+template <int G>
+__device__ __forceinline__ void attn_partial_mfma(const bf16x8_mt (&qb)[4], MfmaKV& t0, const __bf16* __restrict__ kb,
+                                                  int64_t k_sn, const __bf16* __restrict__ vb, int64_t v_sn,
+                                                  int64_t start, int64_t end, float scale, float* __restrict__ ws_m,
+                                                  float* __restrict__ ws_l, float* __restrict__ ws_acc, int64_t row,
+                                                  int nsplit, bool xnew, const float (&qf)[G][8],
+                                                  const float (&xk)[8], const float (&xv)[8], __bf16* __restrict__ out,
+                                                  int64_t o_sh) {
+  constexpr int kW = kAttnThreads / kWave;
+  constexpr int D = 128;
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  __shared__ float lds_p[kW][kMfmaSlots * 16];
+
+  float m = -INFINITY, l = 0.f, acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  if (xnew && wave == 0) {  // block-uniform: (s, 1, v) of the new token, v counted in lane group 0 only
+    float sg[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float p = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p = fmaf(qf[g][e], xk[e], p);
+      sg[g] = group_sum<16>(p) * scale;
+    }
+    const int h = lane & 15;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (h == g) m = sg[g];
+    l = h < G ? 1.f : 0.f;
+    if (h >= G) m = -INFINITY;
+    if ((lane >> 4) == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = xv[e];
+    }
+  }
+
+  // Two register buffers in pairs of tiles, as attn_partial: the loads of the next
+  // tile are issued before the current one is computed.
+  const int64_t step = (int64_t)kMfmaSlots * kW;
+  const int64_t n0 = start + (int64_t)kMfmaSlots * wave;
+  const int64_t nit = end > n0 ? (end - n0 + step - 1) / step : 0;
+  MfmaKV t1;
+  int64_t it = 0;
+#pragma unroll 1
+  for (; it + 2 < nit; it += 2) {
+    mfma_issue(t1, kb, k_sn, vb, v_sn, n0 + (it + 1) * step, end);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_mac<G>(t0, qb, n0 + it * step, end, scale, m, l, acc, lds_p[wave]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_issue(t0, kb, k_sn, vb, v_sn, n0 + (it + 2) * step, end);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_mac<G>(t1, qb, n0 + (it + 1) * step, end, scale, m, l, acc, lds_p[wave]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (it + 1 < nit) {
+    mfma_issue(t1, kb, k_sn, vb, v_sn, n0 + (it + 1) * step, end);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_mac<G>(t0, qb, n0 + it * step, end, scale, m, l, acc, lds_p[wave]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_mac<G>(t1, qb, n0 + (it + 1) * step, end, scale, m, l, acc, lds_p[wave]);
+  } else if (it < nit) {
+    mfma_mac<G>(t0, qb, n0 + it * step, end, scale, m, l, acc, lds_p[wave]);
+  }
+
+  // The four lane groups of a wavefront hold sums over disjoint slots under one max.
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      LanePair q2 = pair16(acc[g][e]);
+      const float a2 = q2.lo + q2.hi;
+      q2 = pair32(a2);
+      acc[g][e] = q2.lo + q2.hi;
+    }
+  // Block merge of the kW streams against their largest max, in wavefront order.
+  __shared__ float sm_max[kW][G];
+  __shared__ float sm_l[kW][G];
+  __shared__ float sm_acc[kW][G][D];
+  float mg[G], lg[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mg[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), g));
+    lg[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), g));
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) sm_max[wave][g] = mg[g];
+  }
+  lds_barrier();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mb = sm_max[0][g];
+#pragma unroll
+    for (int j = 1; j < kW; ++j) mb = fmaxf(mb, sm_max[j][g]);
+    const float w = mg[g] == -INFINITY ? 0.f : exp2f((mg[g] - mb) * kLog2e);
+    if (lane < 16) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm_acc[wave][g][8 * lane + e] = acc[g][e] * w;
+    }
+    if (lane == 0) sm_l[wave][g] = lg[g] * w;
+  }
+  lds_barrier();
+  for (int i = tid; i < G * D; i += kAttnThreads) {
+    const int g = i / D;
+    const int d = i % D;
+    float mx = sm_max[0][g];
+#pragma unroll
+    for (int j = 1; j < kW; ++j) mx = fmaxf(mx, sm_max[j][g]);
+    float a = 0.f, ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < kW; ++j) {
+      a += sm_acc[j][g][d];
+      ls += sm_l[j][g];
+    }
+    if (out) {
+      Elem<__bf16>::store1(out + (int64_t)g * o_sh + d, a / ls);
+      continue;
+    }
+    const int64_t slot = row + (int64_t)g * nsplit;
+    ws_acc[slot * D + d] = a;
+    if (d == 0) {
+      ws_m[slot] = mx;
+      ws_l[slot] = ls;
+    }
+  }
+}
+
 // The partial-softmax reduce of one (row, query head),
 //   out[d] = sum_s w_s acc_s[d] / sum_s w_s l_s,  w_s = exp(m_s - max_j m_j),
 // for all D elements by a block of NT threads. The splits are dealt round-robin to NT / D thread groups (one thread

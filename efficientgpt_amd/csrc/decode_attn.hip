@@ -49,6 +49,34 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(
   int64_t start, end;
   attn_split_range(len, nsplit, split, start, end);
 
+  if constexpr (kAttnMfma<T, D, G>) {
+    // q . k on MFMA: the B fragments of Q^T straight from q (column h = lane % 16 is
+    // query head hk * G + h; zero past the group), then the first K/V tile.
+    const int lane = threadIdx.x % kWave;
+    const int h = lane & 15;
+    bf16x8_mt qb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 z{0u, 0u, 0u, 0u};
+      const u32x4 v = ld16(q + (int64_t)b * q_sb + (int64_t)(hk * G + (h < G ? h : 0)) * q_sh + 32 * c + 8 * (lane >> 4));
+      qb[c] = __builtin_bit_cast(bf16x8_mt, h < G ? v : z);
+    }
+    const __bf16* kbb = (const __bf16*)(k + (int64_t)b * k_sb + (int64_t)hk * k_sh);
+    const __bf16* vbb = (const __bf16*)(v + (int64_t)b * v_sb + (int64_t)hk * v_sh);
+    MfmaKV t0;
+    mfma_issue(t0, kbb, k_sn, vbb, v_sn, start + kMfmaSlots * (int)(threadIdx.x / kWave), end);
+    const float none[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float qnone[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qnone[g][e] = 0.f;
+    __bf16* o = nsplit == 1 ? (__bf16*)out + (int64_t)b * o_sb + (int64_t)(hk * G) * o_sh : nullptr;
+    attn_partial_mfma<G>(qb, t0, kbb, k_sn, vbb, v_sn, start, end, scale, ws_m, ws_l, ws_acc,
+                         ((int64_t)b * Hq + hk * G) * nsplit + split, nsplit, false, qnone, none, none, o, o_sh);
+    return;
+  }
+
   u32x4 qr[G][LPR];
 #pragma unroll
   for (int g = 0; g < G; ++g)

@@ -545,8 +545,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
 
   uint16_t* kc = a.k_cache + (int64_t)hk * a.c_sh;
   uint16_t* vc = a.v_cache + (int64_t)hk * a.c_sh;
+  constexpr bool kMfma = kAttnMfma<__bf16, D, G>;
   AttnPipe<1, 4> pp;
-  attn_begin<Geo>(pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached);
+  MfmaKV t0;
+  if constexpr (kMfma) {
+    mfma_issue(t0, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start + kMfmaSlots * (tid / kWave),
+               end_cached);
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    attn_begin<Geo>(pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached);
+  }
 
   float qf[G][EPL];
 #pragma unroll
@@ -565,9 +573,39 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
     }
   }
 
-  attn_partial<Geo, __bf16, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
-                             a.scale, a.ws_m, a.ws_l, a.ws_acc, (int64_t)hq0 * a.nsplit + split, a.nsplit,
-                             owner, kn, vn);
+  if constexpr (kMfma) {
+    // B fragments of Q^T from the rotated queries: each wavefront stages its own
+    // copy (every lane group holds all of them) in LDS and reads column lane % 16.
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    __shared__ __align__(16) uint16_t qs[kAttnThreads / kWave][G][D];
+    if (lane < 16) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        uint32_t pk[4];
+        pack_bf16<EPL>(qf[g], pk);
+        *(u32x4*)&qs[wave][g][d0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    const int h = lane & 15;
+    bf16x8_mt qb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 z{0u, 0u, 0u, 0u};
+      const u32x4 v = *(const u32x4*)&qs[wave][h < G ? h : 0][32 * c + 8 * (lane >> 4)];
+      qb[c] = __builtin_bit_cast(bf16x8_mt, h < G ? v : z);
+    }
+    attn_partial_mfma<G>(qb, t0, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached, a.scale,
+                         a.ws_m, a.ws_l, a.ws_acc, (int64_t)hq0 * a.nsplit + split, a.nsplit, owner, qf, kn, vn,
+                         nullptr, 0);
+  } else {
+    attn_partial<Geo, __bf16, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
+                               a.scale, a.ws_m, a.ws_l, a.ws_acc, (int64_t)hq0 * a.nsplit + split, a.nsplit,
+                               owner, kn, vn);
+  }
 }
 
 // Merge of the split partials: one block per query head.
