@@ -70,6 +70,10 @@ def parse():
                     help='skip the Qwen3-8B long-context measurement (8192-token prompt)')
     ap.add_argument('--no-stream', action='store_true', help='skip the streamed generate() measurement')
     ap.add_argument('--no-extra', action='store_true', help='skip the attention and copy measurements')
+    ap.add_argument('--attention-only', default=None, metavar='L[,L...]',
+                    help='instead of the decode benchmark: the stand-alone split-K attention at these cache lengths '
+                         '(one JSON line each, cold), with --heads query / kv heads at head_dim 128')
+    ap.add_argument('--heads', default='16/8', help='query / kv heads for --attention-only (default 16/8)')
     ap.add_argument('--dispatch-grid', action='store_true',
                     help='instead of the decode benchmark: single-pass against default split-K decode attention over '
                          'batch x heads x cache length (one JSON line per point), the data behind the split policy')
@@ -531,6 +535,15 @@ def main():
     if args.dispatch_grid:
         torch.cuda.set_device(0)
         dispatch_grid()
+        return
+    if args.attention_only:
+        torch.cuda.set_device(0)
+        hq, hkv = (int(v) for v in args.heads.split('/'))
+        with torch.inference_mode():
+            for L in (int(v) for v in args.attention_only.split(',')):
+                r = attention_roofline(L=L, hq=hq, hkv=hkv, copies=max(4, (1 << 29) // (4096 * L) + 1), reps=5)
+                r['heads'] = f'{hq}/{hkv}'
+                print(json.dumps(r), flush=True)
         return
     from efficientgpt_amd.fast_decode import GraphGreedyDecoder
     from efficientgpt_amd.qwen3 import QWEN3_1_7B, QWEN3_8B, Qwen3Int8Engine

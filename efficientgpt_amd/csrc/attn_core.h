@@ -417,6 +417,12 @@ template <typename T, int D, int G>
 constexpr bool kAttnMfma = __is_same(T, __bf16) && D == 128 && G == 4;
 
 constexpr int kMfmaSlots = 16;  // slots of one wavefront tile
+// The wavefront's p tile in LDS: p(slot s, head h) at (s % 4) * 68 + (s / 4) * 16 + h.
+// Lanes store p of slots 4 (l / 16) + r (one r at a time: 64 consecutive words) and
+// read the G heads of slot 4 t + l / 16 (the four lane groups 68 words apart: four
+// distinct banks), so neither side conflicts on banks.
+constexpr int kPTileStride = 68;
+constexpr int kPTileWords = 4 * kPTileStride;
 
 struct MfmaKV {
   u32x4 k[4];  // A operand: 16 slots x 32 dims per chunk
@@ -471,7 +477,7 @@ __device__ __forceinline__ void mfma_mac(const MfmaKV& t, const bf16x8_mt (&qb)[
   for (int r = 0; r < 4; ++r) {
     const float p = exp2_softmax((sv[r] - mref) * kLog2e);  // 0 for masked slots
     ps += p;
-    lds_p[(4 * (lane >> 4) + r) * 16 + (lane & 15)] = p;
+    lds_p[r * kPTileStride + (lane >> 4) * 16 + (lane & 15)] = p;
   }
   pr = pair16(ps);
   ps = pr.lo + pr.hi;
@@ -483,17 +489,24 @@ __device__ __forceinline__ void mfma_mac(const MfmaKV& t, const bf16x8_mt (&qb)[
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  float ag[G];
+  bool same = true;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float ag = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+    ag[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+    same = same && ag[g] == 1.f;
+  }
+  if (!same) {  // wave-uniform: once the running maxima settle, alpha is exactly 1 and acc needs no rescale
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= ag[g];
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float vf[8];
     Elem<__bf16>::unpack(t.v[r], vf);
-    const float* prow = lds_p + (4 * r + (lane >> 4)) * 16;
+    const float* prow = lds_p + (lane >> 4) * kPTileStride + r * 16;
     float pg[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) pg[g] = prow[g];
@@ -529,7 +542,7 @@ __device__ __forceinline__ void attn_partial_mfma(const bf16x8_mt (&qb)[4], Mfma
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
-  __shared__ float lds_p[kW][kMfmaSlots * 16];
+  __shared__ float lds_p[kW][kPTileWords];
 
   float m = -INFINITY, l = 0.f, acc[G][8];
 #pragma unroll
