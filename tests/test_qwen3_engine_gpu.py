@@ -103,15 +103,17 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
     assert agree / total >= 0.95, agree / total
 
 
-@pytest.mark.parametrize('shape,std,cap', [(TINY, 0.2, 96), (SMALL, 0.15, 96), (SMALL, 0.15, 2048), (TINY, 0.2, 4096),
-                                           (SMALL8, 0.15, 96), (SMALL8, 0.15, 4096)])
-def test_fused_step_matches_unfused_step(shape, std, cap):
+@pytest.mark.parametrize('shape,std,cap,plen', [(TINY, 0.2, 96, 9), (SMALL, 0.15, 96, 9), (SMALL, 0.15, 2048, 9),
+                                                (SMALL, 0.15, 2048, 1500), (TINY, 0.2, 4096, 9),
+                                                (SMALL8, 0.15, 96, 9), (SMALL8, 0.15, 2048, 1500),
+                                                (SMALL8, 0.15, 4096, 9)])
+def test_fused_step_matches_unfused_step(shape, std, cap, plen):
     """The fused step against the one-kernel-per-op step on the same tokens. Up to 2048 slots the attention blocks
-    serve one query head and the o_proj GEMV merges their 2 or 8 splits; at 4096 slots (32 splits, TINY 64) the blocks
-    serve a kv head's whole group and a launch of its own merges the splits. SMALL8 runs 4 query heads per kv head,
-    as Qwen3-8B does."""
+    serve one query head and the o_proj GEMV merges their 2 or 8 splits (a 1500-token prompt fills the 8 splits of
+    a 2048-slot cache: about 190 slots each); at 4096 slots (32 splits, TINY 64) the blocks serve a kv head's whole
+    group and a launch of its own merges the splits. SMALL8 runs 4 query heads per kv head, as Qwen3-8B does."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
-    prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(3))
+    prompt = torch.randint(0, shape.vocab, (plen,), generator=torch.Generator().manual_seed(3))
     runs = {}
     for name, fn in (('unfused', eng.step_unfused), ('fused', eng.step)):
         eng.reset()
@@ -128,11 +130,11 @@ def test_fused_step_matches_unfused_step(shape, std, cap):
         runs[name] = (toks, logits, eng.k_cache.float().cpu().clone(), eng.v_cache.float().cpu().clone(),
                       int(eng.position))
     (tu, lu, ku, vu, pu), (tf, lf, kf, vf, pf) = runs['unfused'], runs['fused']
-    assert pu == pf == 9 + 12
+    assert pu == pf == plen + 12
     for a, b in zip(lu, lf):
         assert float((a - b).abs().max()) <= 2e-2 * float(a.abs().max())
     assert float((ku - kf).abs().max()) <= 2e-2 * float(ku.abs().max())
-    assert torch.equal(vu[:, :, :9], vf[:, :, :9])  # prompt slots come from the same prefill
+    assert torch.equal(vu[:, :, :plen], vf[:, :, :plen])  # prompt slots come from the same prefill
     assert float((vu - vf).abs().max()) <= 2e-2 * float(vu.abs().max())
     agree = sum(a == b for a, b in zip(tu, tf))
     assert agree >= 11, (tu, tf)
@@ -182,6 +184,27 @@ def test_qwen3_8b_widths_match_oracle():
         assert float((got - want).abs().max()) <= 2e-2 * float(want.abs().max()), cap
         del eng, orc
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize('shape', [SMALL, SMALL8])
+def test_long_prompt_in_2048_slots_matches_oracle(shape):
+    """A 1500-token prompt in a 2048-slot cache: the step's 8 splits of one-query-head blocks each hold about 190
+    slots, merged in the o_proj GEMV. Teacher-forced greedy steps and the last step's logits against the oracle."""
+    eng, orc = build(shape, seed=29, std=0.15, cap=2048)
+    prompt = torch.randint(0, shape.vocab, (1500,), generator=torch.Generator().manual_seed(8))
+    ref, margins, tops = oracle_greedy_with_margins(orc, prompt, 10)
+    assert len(set(ref)) > 4
+    a, n, bad = teacher_forced_agreement(eng, prompt, ref, margins, tops)
+    assert not bad, bad
+    assert a >= n - 1, (a, n)
+    orc.reset()
+    logits, pos = orc.forward(prompt, 0), len(prompt)
+    for t in ref[:-1]:
+        logits = orc.forward([t], pos)
+        pos += 1
+    got = eng.logits[0].float().cpu()
+    want = logits.float()
+    assert float((got - want).abs().max()) <= 2e-2 * float(want.abs().max())
 
 
 @pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL8, 96), (SMALL, 2048), (SMALL8, 4096)])
