@@ -180,6 +180,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// int8 GEMV of 2 to kGemvFewRowsMax rows (qwen3_fused.hip): y rows ldy apart
+// from x rows ldx apart, each row bit-identical to a one-row egpt_int8_gemv.
+// EGPT_ERR_UNSUPPORTED for shapes it does not take (K not a multiple of 16 or
+// past 12288, unaligned rows).
+constexpr int kGemvFewRowsMax = 4;
+// egpt_int8_gemv gives 3-4 rows to gemv_few_rows below this many features, where
+// a wavefront owns one weight row and the launch is latency-bound (Qwen3-1.7B's
+// o_proj and down_proj at 4 rows: 3.9 / 7.0 us against 4.1 / 8.2 us on MFMA); at
+// and above it the conversion and four FMAs per weight byte bound the vector
+// kernel, and MFMA is faster (QKV 4.4 / gate_up 8.2 / lm_head 86 us against 4.9 /
+// 9.2 / 89 us).
+constexpr int kGemvFewRowsWideN = 4096;
+int gemv_few_rows(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y, int64_t ldy,
+                  int M, int N, int K, hipStream_t st);
+
 }  // namespace egpt
 
 // Map a HIP launch result to the library's status convention.

@@ -383,9 +383,16 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
     d.y = y;
     return egpt_int8_gemv_fused(&d, stream);
   }
+  if ((M == 2 || (M <= kGemvFewRowsMax && N < kGemvFewRowsWideN)) && K >= 16 && K % 16 == 0 && K <= kFusedMaxK &&
+      ldw % 16 == 0 && ldx % 8 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)x % 16 == 0) {
+    // 2 aligned rows, or 3-4 over narrow outputs: the single-row kernel's weight
+    // stream with the rows in LDS, each weight converted once (each output row
+    // bit-identical to a one-row call).
+    return gemv_few_rows(x, ldx, w, ldw, scale, y, ldy, M, N, K, stream);
+  }
   if (M >= 3 && K >= 64 && K % 64 == 0 && ldw % 16 == 0 && ldx % 8 == 0 && (uintptr_t)w % 16 == 0 &&
       (uintptr_t)x % 16 == 0) {
-    // 3-16 rows: MFMA (two rows stay on the vector kernel, which is faster there)
+    // 3-16 rows (3-4 over wide outputs): MFMA
     const uint16_t* xx = (const uint16_t*)x;
     uint16_t* yy = (uint16_t*)y;
     // all 8 wavefronts on one 16-feature group: splitting K eight ways keeps the most

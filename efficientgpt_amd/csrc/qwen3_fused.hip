@@ -52,6 +52,7 @@ struct FusedGemv {
   int N;                   // output features
   int K;
   uint16_t* y;             // output row (Argmax: the logits, may be null)
+  int64_t y_ld;            // two-row GEMV: row stride of y (x rows are x_ld apart)
   const uint16_t* resid;   // Resid: residual row, or a table when resid_token is set
   const int64_t* resid_token;
   int64_t resid_ld;
@@ -452,6 +453,141 @@ __global__ __launch_bounds__(W * kWave) void fused_gemv_kernel(const FusedGemv a
       a.part_v[blockIdx.x] = best.v;
       a.part_i[blockIdx.x] = best.i;
     }
+  }
+}
+
+// ---------------------------------------------------------------- 2-4 activation rows
+//
+// y[m, n] = bf16(scale[n] * sum_k x[m, k] w[n, k]) for m < M (2 to 4): the
+// reference's decode contract (research/realmodel/int8_linear.py:26-38) at a
+// few rows. The weights stream as in fused_gemv_kernel (stages of CG chunks in
+// two ping-pong register buffers, unconditional loads, exact waits), the M
+// activation rows are staged in LDS, and each weight byte is converted once and
+// multiplied into every row. Per row, the chunk sums and the row reduction are
+// the single-row kernel's in the same order, so each output row is bit-identical
+// to a one-row call on that row.
+
+// acc[m] += w * x[m] over one 16-byte weight load, biased form, in
+// dot16_biased's order for each row.
+template <int M>
+__device__ __forceinline__ void dot16_biased_rows(const u32x4 wq, const float (&x)[M][16], float (&acc)[M]) {
+  const uint32_t d[4] = {wq.x ^ 0x80808080u, wq.y ^ 0x80808080u, wq.z ^ 0x80808080u, wq.w ^ 0x80808080u};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float wv = (float)((d[j] >> (8 * b)) & 0xffu);
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[m] = fmaf(wv, x[m][4 * j + b], acc[m]);
+    }
+  }
+}
+
+template <int M, int R, int CG>
+__device__ __forceinline__ void stage_mac_rows(const GemvStage<R, CG>& s, const uint16_t* hs, int ldh, int c0,
+                                               int lane, float (&acc)[R][M], float (&sx)[M]) {
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int k = (c0 + c) * kFChunk + lane * 16;
+    float x[M][16];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      unpack_bf16x16(*(const u32x4*)(hs + m * ldh + k), *(const u32x4*)(hs + m * ldh + k + 8), x[m]);
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) t += x[m][e];
+      sx[m] += t;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) dot16_biased_rows<M>(s.w[c][r], x, acc[r]);
+  }
+}
+
+// Stages of the few-rows kernel: the single-row kernel's, halved for two weight
+// rows per wavefront over rows of 8 chunks or more (their full-size stages need
+// more than 256 VGPRs with several activation rows and spill).
+constexpr int rows_stage_chunks(int R, int NCH) { return stage_chunks(R >= 2 && NCH >= 8 ? 2 * R : R, NCH); }
+
+template <int M, int R, int NCH, int W>
+__global__ __launch_bounds__(W * kWave) void gemv_rows_kernel(const FusedGemv a) {
+  constexpr int CG = rows_stage_chunks(R, NCH);
+  constexpr int NST = NCH / CG;
+  constexpr int NT = W * kWave;
+  constexpr int KP = NCH * kFChunk;  // LDS row: K rounded up to whole chunks, zero past K
+  constexpr int kPasses = (KP + NT * 8 - 1) / (NT * 8);
+  using Stage = GemvStage<R, CG>;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int64_t t = (int64_t)blockIdx.x * W + tid / kWave;
+  const u32x4 z{0u, 0u, 0u, 0u};
+
+  // Activation loads first (they retire first), then the weight stream.
+  u32x4 xv[M][kPasses];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int k8 = (p * NT + tid) * 8;
+      xv[m][p] = k8 < a.K ? ld16(a.x + m * a.x_ld + k8) : z;
+    }
+  const int8_t* rows[R];
+  tile_rows<R, kEpiStore>(a, t, rows);
+  Stage buf[2];
+  buf[0].load(a, rows, 0, lane);
+  const GemvEpi ep = tile_epi<R, kEpiStore>(a, t, lane);
+  __shared__ __align__(16) uint16_t hs[M * KP];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int k8 = (p * NT + tid) * 8;
+      if (k8 < KP) *(u32x4*)(hs + m * KP + k8) = xv[m][p];
+    }
+  lds_barrier();
+  if (t * R >= a.N) return;  // a wavefront past the last tile (no barrier follows)
+
+  float acc[R][M], sx[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    sx[m] = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][m] = 0.f;
+  }
+  int st = 0;
+#pragma unroll 1
+  for (; st + 2 < NST; st += 2) {
+    buf[1].load(a, rows, (st + 1) * CG, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_mac_rows<M, R, CG>(buf[0], hs, KP, st * CG, lane, acc, sx);
+    __builtin_amdgcn_sched_barrier(0);
+    buf[0].load(a, rows, (st + 2) * CG, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_mac_rows<M, R, CG>(buf[1], hs, KP, (st + 1) * CG, lane, acc, sx);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (NST % 2 == 0) {
+    buf[1].load(a, rows, (NST - 1) * CG, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_mac_rows<M, R, CG>(buf[0], hs, KP, (NST - 2) * CG, lane, acc, sx);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_mac_rows<M, R, CG>(buf[1], hs, KP, (NST - 1) * CG, lane, acc, sx);
+  } else {
+    stage_mac_rows<M, R, CG>(buf[0], hs, KP, (NST - 1) * CG, lane, acc, sx);
+  }
+  float mine[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) mine[m] = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float v = wave_sum(acc[r][m] - 128.f * sx[m]);
+      if (lane == r) mine[m] = v;
+    }
+  const int64_t f = t * R + lane;
+  if (lane < R && f < a.N) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) a.y[m * a.y_ld + f] = f32_to_bf16(mine[m] * ep.sc);
   }
 }
 
@@ -917,6 +1053,52 @@ void step_gemvs(const egpt_qwen3_step* s, egpt_gemv_fused* out) {
 }  // namespace
 
 size_t fused_step_bytes(const egpt_qwen3_step* s) { return step_layout(s).total; }
+
+int gemv_few_rows(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y, int64_t ldy,
+                  int M, int N, int K, hipStream_t st) {
+  if (!x || !w || !scale || !y || M < 2 || M > kGemvFewRowsMax || N < 1 || K < 16 || K % 16 ||
+      K > kMaxChunks * kFChunk || ldw < K || ldx < K || ldy < N || ldw % 16 || ldx % 8 || !aligned16(x) ||
+      !aligned16(w))
+    return EGPT_ERR_UNSUPPORTED;
+  FusedGemv a{};
+  a.x = (const uint16_t*)x;
+  a.x_ld = ldx;
+  a.w = w;
+  a.ldw = ldw;
+  a.scale = scale;
+  a.N = N;
+  a.K = K;
+  a.y = (uint16_t*)y;
+  a.y_ld = ldy;
+  const int r = features_per_wave(N, false);  // the single-row kernel's tiles
+  const unsigned blocks = gemv_blocks(N, false, false);
+  constexpr int W = kGemvWaves;
+  const int nch = chunks_for(K);
+#define EGPT_ROWS(MM, RR, C) hipLaunchKernelGGL((gemv_rows_kernel<MM, RR, C, W>), dim3(blocks), dim3(W * kWave), 0, st, a)
+#define EGPT_CHUNKS(MM, RR)                                            \
+  switch (nch) {                                                       \
+    case 1: EGPT_ROWS(MM, RR, 1); break;                               \
+    case 2: EGPT_ROWS(MM, RR, 2); break;                               \
+    case 3: EGPT_ROWS(MM, RR, 3); break;                               \
+    case 4: EGPT_ROWS(MM, RR, 4); break;                               \
+    case 6: EGPT_ROWS(MM, RR, 6); break;                               \
+    case 8: EGPT_ROWS(MM, RR, 8); break;                               \
+    case 12: EGPT_ROWS(MM, RR, 12); break;                             \
+    default: return EGPT_ERR_UNSUPPORTED;                              \
+  }
+  switch (M * 2 + (r >= 2 ? 1 : 0)) {
+    case 4: EGPT_CHUNKS(2, 1) break;
+    case 5: EGPT_CHUNKS(2, 2) break;
+    case 6: EGPT_CHUNKS(3, 1) break;
+    case 7: EGPT_CHUNKS(3, 2) break;
+    case 8: EGPT_CHUNKS(4, 1) break;
+    case 9: EGPT_CHUNKS(4, 2) break;
+    default: return EGPT_ERR_UNSUPPORTED;
+  }
+#undef EGPT_CHUNKS
+#undef EGPT_ROWS
+  return EGPT_LAUNCH_STATUS();
+}
 int qwen3_check_step(const egpt_qwen3_step* s) { return check_step(s); }
 
 }  // namespace egpt

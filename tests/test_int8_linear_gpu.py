@@ -193,11 +193,42 @@ def test_single_row_matches_row_kernel_bitwise(k, n):
     check_against_oracle(one.cpu(), x.cpu(), q.cpu(), s.cpu())
 
 
+@pytest.mark.parametrize('m', [2, 3, 4])
+@pytest.mark.parametrize('k,n', [(2048, 4096), (2048, 2048), (2048, 12288), (6144, 2048), (12288, 4096), (12288, 2048),
+                                 (2064, 48), (1024, 100), (16, 7)])
+def test_few_rows_equal_one_row_calls_bitwise(m, k, n):
+    """Two aligned rows, and 3-4 rows under 4096 features, take the few-rows kernel: the one-row kernel's
+    weight stream with the activation rows in LDS. Each row's chunk sums and row reduction run in the one-row
+    kernel's order, so each output row must equal a one-row call on that row bit for bit; with strided rows
+    (ldx > K, ldy > N) too. 3-4 rows over 4096 features or more take the MFMA kernel: oracle check only."""
+    from efficientgpt_amd import _lib
+    from efficientgpt_amd.int8_linear import int8_matmul
+    x, q, s = make_case(m, k, n, seed=k * 3 + n + m)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    few = int8_matmul(xd, qd, sd)
+    check_against_oracle(few.cpu(), x, q, s)
+    if m > 2 and n >= 4096:
+        return
+    ones = torch.cat([int8_matmul(xd[i:i + 1].contiguous(), qd, sd) for i in range(m)])
+    assert torch.equal(few, ones)
+    # strided rows: x rows 2k + 16 apart, y rows n + 5 apart
+    xs = torch.zeros(m, 2 * k + 16, dtype=torch.bfloat16, device='cuda')
+    xs[:, :k] = xd
+    ys = torch.full((m, n + 5), 7.0, dtype=torch.bfloat16, device='cuda')
+    _lib.check('egpt_int8_gemv', _lib.lib().egpt_int8_gemv(xs.data_ptr(), xs.stride(0), qd.data_ptr(), k,
+                                                             sd.data_ptr(), ys.data_ptr(), ys.stride(0), m, n, k,
+                                                             _lib.stream_ptr()))
+    torch.cuda.synchronize()
+    assert torch.equal(ys[:, :n], few)
+    assert bool((ys[:, n:] == 7.0).all())  # nothing written past N
+
+
 @pytest.mark.parametrize('m', [3, 4, 8, 16])
 @pytest.mark.parametrize('k,n', [(2048, 4096), (6144, 2048), (2048, 100), (12288, 48), (512, 32768)])
 def test_small_batch_mfma_kernel_matches_oracle(m, k, n):
-    """3-16 rows take the MFMA kernel (K a multiple of 64, aligned rows): against the oracle's decode
-    rule, odd N, the longest K, and 2048 feature groups (32768 features)."""
+    """3-16 rows take the MFMA kernel (K a multiple of 64, aligned rows; 3-4 rows under 4096 features the
+    few-rows kernel): against the oracle's decode rule, odd N, the longest K, and 2048 feature groups
+    (32768 features)."""
     from efficientgpt_amd.int8_linear import int8_matmul
     x, q, s = make_case(m, k, n, seed=100 + m + k + n)
     xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
