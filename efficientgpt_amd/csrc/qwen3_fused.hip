@@ -655,13 +655,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
   const int split = blockIdx.y;
   const int Hq = a.Hkv * a.group;
 
+  constexpr bool kMfma = kAttnMfma<__bf16, D, G>;
+  // The MFMA form normalises and rotates each head once per block: lane group
+  // grp (16 lanes, one 128-element row) takes query head hq0 + grp for grp < G
+  // and the new key otherwise, and the block shares them through LDS. The vector
+  // form keeps every head in every group's registers (its loop reads them there).
+  const int grp = tid / LPS;
+  constexpr int GQ = kMfma ? 1 : G;  // query rows each thread normalises
+
   // The rows that do not depend on the position go out before it is read.
-  u32x4 qr[G], qw, kw, kr, vr, cr, sr;
+  u32x4 qr[GQ], qw, kw, kr, vr, cr, sr;
+  if constexpr (kMfma) {
+    const bool qrow = grp < G;
+    qr[0] = ld16(a.qkv + (int64_t)(qrow ? hq0 + grp : Hq + hk) * D + d0);
+    qw = ld16((qrow ? a.q_norm_w : a.k_norm_w) + d0);
+  } else {
 #pragma unroll
-  for (int g = 0; g < G; ++g) qr[g] = ld16(a.qkv + (int64_t)(hq0 + g) * D + d0);
-  qw = ld16(a.q_norm_w + d0);
-  kw = ld16(a.k_norm_w + d0);
-  kr = ld16(a.qkv + (int64_t)(Hq + hk) * D + d0);
+    for (int g = 0; g < G; ++g) qr[g] = ld16(a.qkv + (int64_t)(hq0 + g) * D + d0);
+    qw = ld16(a.q_norm_w + d0);
+    kw = ld16(a.k_norm_w + d0);
+    kr = ld16(a.qkv + (int64_t)(Hq + hk) * D + d0);
+  }
   vr = ld16(a.qkv + (int64_t)(Hq + a.Hkv + hk) * D + d0);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -681,7 +695,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
 
   uint16_t* kc = a.k_cache + (int64_t)hk * a.c_sh;
   uint16_t* vc = a.v_cache + (int64_t)hk * a.c_sh;
-  constexpr bool kMfma = kAttnMfma<__bf16, D, G>;
   AttnPipe<1, 4> pp;
   MfmaKV t0;
   if constexpr (kMfma) {
@@ -692,52 +705,60 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
     attn_begin<Geo>(pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached);
   }
 
-  float qf[G][EPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) head_norm_rope<D, EPL, LPS>(qr[g], qw, cr, sr, d0, a.eps, qf[g]);
   float kn[EPL], vn[EPL];
-  if (owner) {
-    head_norm_rope<D, EPL, LPS>(kr, kw, cr, sr, d0, a.eps, kn);
-    Elem<__bf16>::unpack(vr, vn);
-    if (tid < LPS && hq0 % a.group == 0) {  // one block of the kv head stores it
-      uint32_t packed[EPL / 2];
-#pragma unroll
-      for (int e = 0; e < EPL / 2; ++e)
-        packed[e] = (uint32_t)f32_to_bf16(kn[2 * e]) | ((uint32_t)f32_to_bf16(kn[2 * e + 1]) << 16);
-      *(u32x4*)(kc + pos * a.c_sn + d0) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-      *(u32x4*)(vc + pos * a.c_sn + d0) = vr;
-    }
-  }
-
   if constexpr (kMfma) {
-    // B fragments of Q^T from the rotated queries: each wavefront stages its own
-    // copy (every lane group holds all of them) in LDS and reads column lane % 16.
+    // This group's head (query hq0 + grp, or the new key) normalised and rotated,
+    // then every head shared through LDS: rows 0..G-1 the queries, row G the key.
     const int lane = tid % kWave;
-    const int wave = tid / kWave;
-    __shared__ __align__(16) uint16_t qs[kAttnThreads / kWave][G][D];
-    if (lane < 16) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        uint32_t pk[4];
-        pack_bf16<EPL>(qf[g], pk);
-        *(u32x4*)&qs[wave][g][d0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
-      }
+    float hv[EPL];
+    head_norm_rope<D, EPL, LPS>(qr[0], qw, cr, sr, d0, a.eps, hv);
+    __shared__ __align__(16) uint16_t qs[G + 1][D];
+    if (grp <= G) {
+      uint32_t pk[EPL / 2];
+      pack_bf16<EPL>(hv, pk);
+      *(u32x4*)&qs[grp][d0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    lds_barrier();
+    // B fragments of Q^T: column lane % 16 is query head lane % 16 (zero past G).
     const int h = lane & 15;
     bf16x8_mt qb[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const u32x4 z{0u, 0u, 0u, 0u};
-      const u32x4 v = *(const u32x4*)&qs[wave][h < G ? h : 0][32 * c + 8 * (lane >> 4)];
+      const u32x4 v = *(const u32x4*)&qs[h < G ? h : 0][32 * c + 8 * (lane >> 4)];
       qb[c] = __builtin_bit_cast(bf16x8_mt, h < G ? v : z);
+    }
+    // This lane's 8 elements of every query and of the key (the new token's
+    // score and the cache write take them in that layout).
+    float qf[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) Elem<__bf16>::unpack(*(const u32x4*)&qs[g][d0], qf[g]);
+    const u32x4 kp = *(const u32x4*)&qs[G][d0];
+    Elem<__bf16>::unpack(kp, kn);
+    Elem<__bf16>::unpack(vr, vn);
+    if (owner && tid < LPS && hq0 % a.group == 0) {  // one block of the kv head stores it
+      *(u32x4*)(kc + pos * a.c_sn + d0) = kp;
+      *(u32x4*)(vc + pos * a.c_sn + d0) = vr;
     }
     attn_partial_mfma<G>(qb, t0, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached, a.scale,
                          a.ws_m, a.ws_l, a.ws_acc, (int64_t)hq0 * a.nsplit + split, a.nsplit, owner, qf, kn, vn,
                          nullptr, 0);
   } else {
+    float qf[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) head_norm_rope<D, EPL, LPS>(qr[g], qw, cr, sr, d0, a.eps, qf[g]);
+    if (owner) {
+      head_norm_rope<D, EPL, LPS>(kr, kw, cr, sr, d0, a.eps, kn);
+      Elem<__bf16>::unpack(vr, vn);
+      if (tid < LPS && hq0 % a.group == 0) {  // one block of the kv head stores it
+        uint32_t packed[EPL / 2];
+#pragma unroll
+        for (int e = 0; e < EPL / 2; ++e)
+          packed[e] = (uint32_t)f32_to_bf16(kn[2 * e]) | ((uint32_t)f32_to_bf16(kn[2 * e + 1]) << 16);
+        *(u32x4*)(kc + pos * a.c_sn + d0) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+        *(u32x4*)(vc + pos * a.c_sn + d0) = vr;
+      }
+    }
     attn_partial<Geo, __bf16, G>(qf, pp, (const __bf16*)kc, a.c_sn, (const __bf16*)vc, a.c_sn, start, end_cached,
                                a.scale, a.ws_m, a.ws_l, a.ws_acc, (int64_t)hq0 * a.nsplit + split, a.nsplit,
                                owner, kn, vn);
