@@ -332,6 +332,42 @@ def gemv_small_batch(floor_us, rows=(1, 2, 4, 8), reps=5):
     return out
 
 
+# The reference's held-out small GEMV shapes (M x K -> N) and its published times on an RTX 4060, L2-warm
+# (runs/20261031_v4/int8_study/heldout_int8_gemv.json; the reference does not claim them as DRAM numbers).
+REFERENCE_HELDOUT_US = {(1, 2048, 2048): 7.6, (2, 2048, 1024): 5.3, (4, 6144, 2048): 20.1, (8, 2048, 6144): 22.2}
+
+
+def gemv_reference_shapes(reps=5):
+    """egpt_int8_gemv at the reference's held-out small shapes, warm (one weight copy, called back to back, so it
+    stays in the caches as the reference's numbers do) and cold (a weight copy per call), beside the reference's
+    published time."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device('cuda')
+    g = torch.Generator(device=dev).manual_seed(2)
+    out = {}
+    for (m, k, n), ref_us in REFERENCE_HELDOUT_US.items():
+        sets = max(2, -(-(600 << 20) // (n * k)))
+        ws = [torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8) for _ in range(sets)]
+        sc = torch.rand(n, generator=g, device=dev) * 1e-3
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+        def run(weights):
+            st = _lib.stream_ptr()
+            for w in weights:
+                _lib.check('egpt_int8_gemv', lib.egpt_int8_gemv(x.data_ptr(), k, w.data_ptr(), k, sc.data_ptr(),
+                                                                y.data_ptr(), n, m, n, k, st))
+
+        cold = _time_graph(lambda: run(ws), reps) / sets
+        warm = _time_graph(lambda: run([ws[0]] * sets), reps) / sets
+        out[f'{m}x{k}->{n}'] = {'us_warm': round(warm * 1e6, 2), 'us_cold': round(cold * 1e6, 2),
+                               'reference_rtx4060_warm_us': ref_us}
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def long_context(prompt_len=8192, steps=32, warmup=4, seed=0):
     """The long-context workload: a random-init Qwen3-8B-architecture int8 model (36 layers, hidden 4096,
     intermediate 12288, 32 q / 8 kv heads) after a `prompt_len`-token uniform-random prompt, cache of prompt + 512
@@ -631,6 +667,7 @@ def main():
                 r['frac_beyond_floor'] = round((4096 * int(L) + 8192) / max(r['us_per_call'] - launches * floor, 1e-3)
                                                / 1e3 / HBM_PEAK_GBPS, 4)
             extra['gemv_small_batch'] = gemv_small_batch(floor)
+            extra['gemv_reference_shapes'] = gemv_reference_shapes()
             extra['prefill_gemm'] = prefill_gemm()
             extra['copy_gbps'] = copy_bandwidth()
     if args.model == 'qwen3-1.7b' and not args.no_long_context:
