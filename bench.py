@@ -698,6 +698,11 @@ def main():
                  'form': 'fused, one launch per phase (egpt_qwen3_decode_step)'},
         'prefill_s': round(prefill_s, 3),
         'streamed_generate': stream,
+        # The reference's own published rate for this decode (other hardware; vs_baseline stays null since no
+        # MI355X figure exists): Qwen3-1.7B int8 with its CUDA-graph decoder, batch 1, 256 new tokens
+        # (the reference's README.md:32-37, BENCHMARK_REPORT.md:22-29).
+        'reference_published': ({'value': 111.9, 'unit': 'tok/s', 'hardware': 'NVIDIA RTX 4060',
+                                 'ratio': round(value / 111.9, 2)} if args.model == 'qwen3-1.7b' else None),
         'build_s': round(build_s, 1),
         **extra,
     }
