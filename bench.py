@@ -66,6 +66,8 @@ def parse():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--cpu-tokens', type=int, default=32,
                     help='greedy tokens in the CPU baseline sample (0: skip; 256 is the full decode of the workload)')
+    ap.add_argument('--cpu-long-tokens', type=int, default=4,
+                    help='CPU decode steps timed on the Qwen3-8B long-context weights (0: skip)')
     ap.add_argument('--no-long-context', action='store_true',
                     help='skip the Qwen3-8B long-context measurement (8192-token prompt)')
     ap.add_argument('--no-stream', action='store_true', help='skip the streamed generate() measurement')
@@ -368,7 +370,40 @@ def gemv_reference_shapes(reps=5):
     return out
 
 
-def long_context(prompt_len=8192, steps=32, warmup=4, seed=0):
+def cpu_long_context(cfg, weights, prompt_len, n_tokens, threads, seed=5):
+    """The CPU oracle on the long-context model's weights, a stated subset of its decode: the 8192-token prefill
+    is not run on the CPU (about 1.3e14 flops); the oracle's cache slots 0..prompt_len-1 are filled with seeded
+    N(0, 1) bf16 keys and values instead, which costs a decode step exactly what the prefilled cache would, and
+    n_tokens greedy steps are timed from position prompt_len. Decode tok/s = n_tokens / time (no TTFT in it)."""
+    from oracle.qwen3 import Qwen3Oracle, Qwen3Shape
+    torch.set_num_threads(threads)
+    shape = Qwen3Shape(cfg.vocab, cfg.hidden, cfg.inter, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                       cfg.rope_theta, cfg.rms_eps, cfg.tied)
+    orc = Qwen3Oracle(shape, weights, dtype=torch.bfloat16, cap=prompt_len + n_tokens + 1)
+    t = time.perf_counter()
+    orc.forward([0], 0)  # builds the cached fp32 images of the int8 weights outside the timed run
+    build_s = time.perf_counter() - t
+    orc.reset()
+    g = torch.Generator().manual_seed(seed)
+    for layer in range(cfg.layers):
+        for cache in (orc.k_cache[layer], orc.v_cache[layer]):
+            cache[:, :prompt_len] = torch.randn(cfg.kv_heads, prompt_len, cfg.head_dim, generator=g).to(cache.dtype)
+    tok, pos = 1, prompt_len
+    t0 = time.perf_counter()
+    for _ in range(n_tokens):
+        tok = int(torch.argmax(orc.forward([tok], pos)))
+        pos += 1
+    dt = time.perf_counter() - t0
+    del orc
+    return {'value': round(n_tokens / dt, 3), 'unit': 'tok/s', 'cores': torch.get_num_threads(), 'kind': 'port',
+            'sample': (f'CPU oracle on the same Qwen3-8B int8 weights (exact fp32 image built in {build_s:.1f} s, '
+                       f'before timing): {n_tokens} greedy decode steps from position {prompt_len} over a cache whose '
+                       f'{prompt_len} slots hold seeded N(0, 1) keys and values (the prefill is not run on the CPU); '
+                       f'{dt:.1f} s'),
+            'cpu': platform.processor() or platform.machine()}
+
+
+def long_context(prompt_len=8192, steps=32, warmup=4, seed=0, cpu_tokens=0):
     """The long-context workload: a random-init Qwen3-8B-architecture int8 model (36 layers, hidden 4096,
     intermediate 12288, 32 q / 8 kv heads) after a `prompt_len`-token uniform-random prompt, cache of prompt + 512
     slots; `steps` graph replays timed back to back. The step's GEMV launches are timed on their own
@@ -377,7 +412,7 @@ def long_context(prompt_len=8192, steps=32, warmup=4, seed=0):
     from efficientgpt_amd.qwen3 import QWEN3_8B, Qwen3Int8Engine
     cfg = QWEN3_8B
     cap = prompt_len + 512
-    eng = Qwen3Int8Engine.random(cfg, cap, seed=seed)
+    eng = Qwen3Int8Engine.random(cfg, cap, seed=seed, keep_weights=cpu_tokens > 0)
     prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=torch.Generator().manual_seed(seed + 1))
     with torch.inference_mode():
         eng.reset()
@@ -405,9 +440,13 @@ def long_context(prompt_len=8192, steps=32, warmup=4, seed=0):
     wbytes, sbytes = cfg.weight_bytes()
     step_bytes = wbytes + sbytes + kv_bytes
     nsplit = eng.nsplit
+    weights = eng.weights if cpu_tokens > 0 else None
     del eng
     torch.cuda.empty_cache()
+    cpu = cpu_long_context(cfg, weights, prompt_len, cpu_tokens, host_threads()) if cpu_tokens > 0 else None
+    del weights
     return {'workload': f'qwen3-8b int8, {prompt_len}-token prompt, cache {cap} slots, {steps} graph replays',
+            'cpu_baseline': cpu,
             'value': round(steps / wall, 2), 'unit': 'tok/s', 'ms_per_step': round(step_ms, 4),
             'prefill_s': round(prefill_s, 3), 'mean_kv_len': mean_len, 'nsplit': nsplit,
             'step_frac': round(step_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -671,7 +710,7 @@ def main():
             extra['prefill_gemm'] = prefill_gemm()
             extra['copy_gbps'] = copy_bandwidth()
     if args.model == 'qwen3-1.7b' and not args.no_long_context:
-        extra['long_context'] = long_context()
+        extra['long_context'] = long_context(cpu_tokens=args.cpu_long_tokens)
     cpu = None
     if args.cpu_tokens > 0 and gpu_tokens and args.model == 'qwen3-1.7b':
         cpu = cpu_baseline(eng, prompt, args.cpu_tokens, gpu_tokens)
