@@ -190,71 +190,93 @@ __device__ __forceinline__ bf16x8_t int8x8_bf16(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(bf16x8_t, u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// G wavefronts share a group of 16 features (8 / G groups per block); with G = 1
-// each wavefront would stream its 16 rows over all of K and store its own outputs.
-template <int G>
+// G wavefronts share FG groups of 16 features (8 / G such sets per block); with
+// G = 1 each wavefront would stream its rows over all of K and store its own
+// outputs. Each activation fragment a wavefront loads feeds the FG groups' MFMAs,
+// so wide outputs read the activations FG times less often per weight byte.
+template <int G, int FG>
 __global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma(
     const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
     const float* __restrict__ scale, uint16_t* __restrict__ y, int64_t ldy, int m_rows, int N, int K) {
-  __shared__ float red[G > 1 ? kMfmaWaves : 1][256];
+  __shared__ float red[G > 1 ? kMfmaWaves : 1][FG * 256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int group = wave / G, sub = wave % G;
-  const int64_t n0 = ((int64_t)blockIdx.x * (kMfmaWaves / G) + group) * 16;
-  const int8_t* wrow = w + min(n0 + lane % 16, (int64_t)N - 1) * ldw + 16 * (lane / 16);
+  const int64_t n0 = ((int64_t)blockIdx.x * (kMfmaWaves / G) + group) * 16 * FG;
+  const int8_t* wrow[FG];
+#pragma unroll
+  for (int f = 0; f < FG; ++f) wrow[f] = w + min(n0 + 16 * f + lane % 16, (int64_t)N - 1) * ldw + 16 * (lane / 16);
   const uint16_t* xrow = x + (int64_t)min(lane % 16, m_rows - 1) * ldx + 16 * (lane / 16);
   const int steps = K / 64;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc[FG];
+#pragma unroll
+  for (int f = 0; f < FG; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   for (int s0 = sub; s0 < steps; s0 += G * kMfmaStage) {
-    u32x4 wv[kMfmaStage], xa[kMfmaStage], xb[kMfmaStage];
+    u32x4 wv[kMfmaStage][FG], xa[kMfmaStage], xb[kMfmaStage];
 #pragma unroll
     for (int j = 0; j < kMfmaStage; ++j) {
       const int st = min(s0 + j * G, steps - 1);  // past the end: a valid step, not accumulated
-      wv[j] = ld16_stream(wrow + st * 64);
+#pragma unroll
+      for (int f = 0; f < FG; ++f) wv[j][f] = ld16_stream(wrow[f] + st * 64);
       xa[j] = ld16(xrow + st * 64);
       xb[j] = ld16(xrow + st * 64 + 8);
     }
 #pragma unroll
     for (int j = 0; j < kMfmaStage; ++j) {
       if (s0 + j * G < steps) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[j]),
-                                                      int8x8_bf16(wv[j].x, wv[j].y), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xb[j]),
-                                                      int8x8_bf16(wv[j].z, wv[j].w), acc, 0, 0, 0);
+#pragma unroll
+        for (int f = 0; f < FG; ++f) {
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[j]),
+                                                           int8x8_bf16(wv[j][f].x, wv[j][f].y), acc[f], 0, 0, 0);
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xb[j]),
+                                                           int8x8_bf16(wv[j][f].z, wv[j][f].w), acc[f], 0, 0, 0);
+        }
       }
     }
   }
   if constexpr (G > 1) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][(4 * (lane / 16) + r) * 16 + lane % 16] = acc[r];
-    __syncthreads();
-    // each group's G partials summed in wavefront order, one output per thread
-    for (int e = threadIdx.x; e < (kMfmaWaves / G) * 256; e += kMfmaWaves * kWave) {
-      const int gi = e / 256, idx = e % 256;
-      float sum = red[gi * G][idx];
+    for (int f = 0; f < FG; ++f)
 #pragma unroll
-      for (int j = 1; j < G; ++j) sum += red[gi * G + j][idx];
+      for (int r = 0; r < 4; ++r) red[wave][f * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = acc[f][r];
+    __syncthreads();
+    // each set's G partials summed in wavefront order, one output per thread
+    for (int e = threadIdx.x; e < (kMfmaWaves / G) * FG * 256; e += kMfmaWaves * kWave) {
+      const int gi = e / (FG * 256), fe = e % (FG * 256);
+      const int f = fe / 256, idx = fe % 256;
+      float sum = red[gi * G][fe];
+#pragma unroll
+      for (int j = 1; j < G; ++j) sum += red[gi * G + j][fe];
       const int m = idx / 16;
-      const int64_t nn = ((int64_t)blockIdx.x * (kMfmaWaves / G) + gi) * 16 + idx % 16;
+      const int64_t nn = ((int64_t)blockIdx.x * (kMfmaWaves / G) + gi) * 16 * FG + 16 * f + idx % 16;
       if (m < m_rows && nn < N) y[(int64_t)m * ldy + nn] = f32_to_bf16(sum * scale[nn]);
     }
   } else {
-    const int64_t n = n0 + lane % 16;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * (lane / 16) + r;
-      if (m < m_rows && n < N) y[(int64_t)m * ldy + n] = f32_to_bf16(acc[r] * scale[n]);
+    for (int f = 0; f < FG; ++f) {
+      const int64_t n = n0 + 16 * f + lane % 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * (lane / 16) + r;
+        if (m < m_rows && n < N) y[(int64_t)m * ldy + n] = f32_to_bf16(acc[f][r] * scale[n]);
+      }
     }
   }
 }
 
-template <int G>
+template <int G, int FG>
 void launch_mfma(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
                  int64_t ldy, int M, int N, int K, hipStream_t st) {
-  const int64_t per_block = 16 * (kMfmaWaves / G);
-  hipLaunchKernelGGL((gemv_i8_mfma<G>), dim3((unsigned)((N + per_block - 1) / per_block)), dim3(kMfmaWaves * kWave),
-                     0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K);
+  const int64_t per_block = 16 * FG * (kMfmaWaves / G);
+  hipLaunchKernelGGL((gemv_i8_mfma<G, FG>), dim3((unsigned)((N + per_block - 1) / per_block)),
+                     dim3(kMfmaWaves * kWave), 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K);
 }
+
+// Feature groups per MFMA wavefront: four for outputs of at least this many
+// features (the lm_head: 151936 x 2048 at 8 rows 75 against 90-99 us, at 4 rows
+// 72-75 against 80 us), one below it, where fewer, wider blocks lose more than the
+// activation reads save (gate_up 12288 x 2048 at two groups: 9.3 against 8.2 us).
+constexpr int64_t kMfmaWideN = 65536;
 
 // Deterministic split-K reduction: fixed split order, then scale, one rounding.
 __global__ __launch_bounds__(256) void gemv_splitk_reduce(const float* __restrict__ part, int splits, int m_rows,
@@ -398,7 +420,8 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
     // all 8 wavefronts on one 16-feature group: splitting K eight ways keeps the most
     // loads in flight (measured faster than 1, 2 or 4 wavefronts per group at every
     // Qwen3-1.7B shape, the 151936-row lm_head included)
-    launch_mfma<kMfmaWaves>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+    if (N >= kMfmaWideN) launch_mfma<kMfmaWaves, 4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+    else launch_mfma<kMfmaWaves, 1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
     return EGPT_LAUNCH_STATUS();
   }
   GemvArgs a{(const uint16_t*)x, ldx, w, ldw, scale, y, ldy, M, N, K, K > 0 ? K : 1, 1};
