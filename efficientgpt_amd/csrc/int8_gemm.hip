@@ -40,33 +40,51 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;        // K per LDS stage of the one-pass kernel: K must be a multiple of it
 constexpr int kBKSplit = 128;  // K per LDS stage of the split-K slices (half the dependent steps)
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int WN, int NW>
 struct GemmShape {
-  static constexpr int TM = BM / 64;  // 32 x 32 tiles per wavefront along M
-  static constexpr int TN = BN / 64;  // ... along N
+  static constexpr int NT = NW * kWave;      // threads of the block
+  static constexpr int WM = NW / WN;          // wavefronts along M (the block's NW as WM x WN)
+  static constexpr int TM = BM / (32 * WM);  // 32 x 32 tiles per wavefront along M
+  static constexpr int TN = BN / (32 * WN);  // ... along N
   static constexpr int kLdsRow = BK + 8;    // bf16 elements per x row in LDS (16 bytes of padding)
   static constexpr int kLdsRowW = BK + 16;  // bytes per int8 weight row in LDS (16 bytes of padding)
-  static constexpr int kALoads = BM * BK * 2 / (kGemmThreads * 16);  // 16-byte x loads per thread per step
-  static constexpr int kBLoads = BN * BK / (kGemmThreads * 16);      // 16-byte int8 loads per thread per step
-  static_assert(TM >= 1 && TN >= 1 && kALoads >= 1 && kBLoads >= 1, "tile too small for the block");
+  static constexpr int kALoads = BM * BK * 2 / (NT * 16);  // 16-byte x loads per thread per step
+  static constexpr int kBLoads = BN * BK / (NT * 16);      // 16-byte int8 loads per thread per step
+  static_assert(WM * WN == NW && TM >= 1 && TN >= 1 && kALoads >= 1 && kBLoads >= 1, "tile too small for the block");
 };
 
 // 8 int8 (one LDS fragment) -> 8 bf16, exact.
+#ifndef EGPT_GEMM_CONV
+#define EGPT_GEMM_CONV 0
+#endif
 __device__ __forceinline__ bf16x8 int8x8_to_bf16(const uint32_t w0, const uint32_t w1) {
   const uint32_t w[2] = {w0, w1};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const float f0 = (float)(int)(int8_t)(w[i] & 0xffu);
-    const float f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
-    const float f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
-    const float f3 = (float)(int)(int8_t)(w[i] >> 24);
-    o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-    o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+    float f0, f1, f2, f3;
+    if constexpr (EGPT_GEMM_CONV == 1) {
+      f0 = (float)__builtin_amdgcn_sbfe((int)w[i], 0, 8);
+      f1 = (float)__builtin_amdgcn_sbfe((int)w[i], 8, 8);
+      f2 = (float)__builtin_amdgcn_sbfe((int)w[i], 16, 8);
+      f3 = (float)((int)w[i] >> 24);
+    } else if constexpr (EGPT_GEMM_CONV == 2) {
+      const uint32_t u = w[i] ^ 0x80808080u;
+      f0 = (float)(u & 0xffu) - 128.f;
+      f1 = (float)((u >> 8) & 0xffu) - 128.f;
+      f2 = (float)((u >> 16) & 0xffu) - 128.f;
+      f3 = (float)(u >> 24) - 128.f;
+    } else {
+      f0 = (float)(int)(int8_t)(w[i] & 0xffu);
+      f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
+      f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
+      f3 = (float)(int)(int8_t)(w[i] >> 24);
+    }
+    o[2 * i] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    o[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
   }
   return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
@@ -84,6 +102,18 @@ struct GemmArgs {
   int splits, kchunk;  // K slices (1: no split) of kchunk columns each, the last one shorter
   float* part;         // splits > 1: fp32 partial tiles [splits][M][N]
 };
+
+// Wavefronts along N of the 128 x 256 and 128 x 128 tiles (the rest of the 4 along M).
+constexpr int kWN256 = 4;
+constexpr int kWN128 = 2;
+// Wavefronts of the 256 x 256 tile and its wave grid.
+constexpr int kNW256x256 = 8;
+constexpr int kWN256x256 = 4;
+
+// Blocks per CU the register allocation must allow (launch bounds): two for the
+// 128 x 256 tile.
+template <int BM, int BN, int NW>
+constexpr int kGemmMinBlocks = (BM == 128 && BN == 256 && NW == 4) ? 2 : 1;
 
 constexpr int kXcds = 8;        // MI355X: 8 XCDs, each with its own L2
 constexpr int kGroupM = 8;      // M tiles per group of the tile order
@@ -107,9 +137,9 @@ __device__ __forceinline__ void gemm_tile(int b, int tiles_m, int tiles_n, int& 
   pid_n = (t % group) / gm;
 }
 
-template <int BM, int BN, int BK, bool SPLIT>
-__global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs a) {
-  using S = GemmShape<BM, BN, BK>;
+template <int BM, int BN, int BK, bool SPLIT, int WN, int NW>
+__global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8_gemm_kernel(const GemmArgs a) {
+  using S = GemmShape<BM, BN, BK, WN, NW>;
   constexpr int TM = S::TM, TN = S::TN;
   constexpr int kLdsRow = S::kLdsRow, kLdsRowW = S::kLdsRowW;
   __shared__ __align__(16) uint16_t As[2][BM * kLdsRow];
@@ -118,8 +148,8 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int wm0 = (wave / 2) * (BM / 2);  // wavefront tile origin in the block tile
-  const int wn0 = (wave % 2) * (BN / 2);
+  const int wm0 = (wave / WN) * (BM / S::WM);  // wavefront tile origin in the block tile
+  const int wn0 = (wave % WN) * (BN / WN);
   const int tiles = a.tiles_m * a.tiles_n;
   const int split = SPLIT ? (int)blockIdx.x / tiles : 0;
   int pid_m, pid_n;
@@ -128,23 +158,26 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   const int64_t n0 = (int64_t)pid_n * BN;
   const int kbeg = SPLIT ? split * a.kchunk : 0;  // this block's K slice [kbeg, kbeg + nk * BK)
 
-  // global -> register staging of one K step
-  const uint16_t* xsrc[S::kALoads];
+  // global -> register staging of one K step: 32-bit byte offsets from the
+  // operands' base pointers (the host checks that both operands span < 2 GiB)
+  const char* xb = (const char*)a.x;
+  const char* wb = (const char*)a.w;
+  uint32_t xoff[S::kALoads];
   int a_lds[S::kALoads];
 #pragma unroll
   for (int j = 0; j < S::kALoads; ++j) {
-    const int i = tid + j * kGemmThreads;
+    const int i = tid + j * S::NT;
     const int row = i / (BK / 8), chunk = i % (BK / 8);
-    xsrc[j] = a.x + min(m0 + row, (int64_t)a.M - 1) * a.ldx + kbeg + chunk * 8;
+    xoff[j] = (uint32_t)((min(m0 + row, (int64_t)a.M - 1) * a.ldx + kbeg + chunk * 8) * 2);
     a_lds[j] = row * kLdsRow + chunk * 8;
   }
-  const int8_t* wsrc[S::kBLoads];
+  uint32_t woff[S::kBLoads];
   int b_lds[S::kBLoads];
 #pragma unroll
   for (int j = 0; j < S::kBLoads; ++j) {
-    const int i = tid + j * kGemmThreads;
+    const int i = tid + j * S::NT;
     const int row = i / (BK / 16), chunk = i % (BK / 16);
-    wsrc[j] = a.w + min(n0 + row, (int64_t)a.N - 1) * a.ldw + kbeg + chunk * 16;
+    woff[j] = (uint32_t)(min(n0 + row, (int64_t)a.N - 1) * a.ldw + kbeg + chunk * 16);
     b_lds[j] = row * kLdsRowW + chunk * 16;
   }
   // Two register staging sets: the loads of step k + 2 are issued while step k is
@@ -154,11 +187,11 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
   const int nk = (SPLIT ? min(a.kchunk, a.K - kbeg) : a.K) / BK;
   u32x4 xr[2][S::kALoads], wr[2][S::kBLoads];
   auto load_step = [&](int kt, int set) {
-    const int k0 = min(kt, nk - 1) * BK;
+    const uint32_t k0 = (uint32_t)(min(kt, nk - 1) * BK);
 #pragma unroll
-    for (int j = 0; j < S::kALoads; ++j) xr[set][j] = ld16(xsrc[j] + k0);
+    for (int j = 0; j < S::kALoads; ++j) xr[set][j] = ld16(xb + (xoff[j] + 2 * k0));
 #pragma unroll
-    for (int j = 0; j < S::kBLoads; ++j) wr[set][j] = ld16_stream(wsrc[j] + k0);
+    for (int j = 0; j < S::kBLoads; ++j) wr[set][j] = ld16_stream(wb + (woff[j] + k0));
   };
   auto store_step = [&](int buf, int set) {
 #pragma unroll
@@ -244,19 +277,26 @@ __global__ __launch_bounds__(kGemmThreads) void int8_gemm_kernel(const GemmArgs 
     }
     return;
   }
-  // y = bf16(bf16(acc) * scale): the reference's two roundings
+  // y = bf16(bf16(acc) * scale): the reference's two roundings. Stores address y
+  // by 32-bit byte offsets from the row of this lane's first accumulator (the
+  // host checks that y spans < 2 GiB); row r of a tile is a constant multiple of
+  // the row pitch away.
+  char* yb = (char*)a.y;
+  const int64_t mrow0 = m0 + wm0 + 4 * (lane / 32);
+  const uint32_t pitch = (uint32_t)(a.ldy * 2);
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     const int64_t n = n0 + wn0 + tn * 32 + lane % 32;
     const float sc = a.scale[min(n, (int64_t)a.N - 1)];
+    const uint32_t base = (uint32_t)((mrow0 * a.ldy + n) * 2);
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm0 + tm * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-        if (m < a.M && n < a.N) {
+        const int dm = tm * 32 + 8 * (r / 4) + r % 4;
+        if (mrow0 + dm < a.M && n < a.N) {
           const float v = bf16_to_f32(f32_to_bf16(acc[tm][tn][r]));
-          a.y[m * a.ldy + n] = f32_to_bf16(v * sc);
+          *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(v * sc);
         }
       }
     }
@@ -285,15 +325,15 @@ unsigned gemm_blocks(const GemmArgs& a) {
   return (unsigned)(((int64_t)a.N + BN - 1) / BN) * (unsigned)(((int64_t)a.M + BM - 1) / BM);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WN = 2, int NW = 4>
 int launch_gemm(GemmArgs a, hipStream_t st) {
   a.tiles_m = (int)(((int64_t)a.M + BM - 1) / BM);
   a.tiles_n = (int)(((int64_t)a.N + BN - 1) / BN);
   const unsigned tiles = (unsigned)a.tiles_m * (unsigned)a.tiles_n;
   if constexpr (BM == 64 && BN == 64) {  // split-K runs 64 x 64 tiles
     if (a.splits > 1) {
-      hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBKSplit, true>), dim3(tiles * (unsigned)a.splits),
-                         dim3(kGemmThreads), 0, st, a);
+      hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBKSplit, true, WN, NW>), dim3(tiles * (unsigned)a.splits),
+                         dim3(NW * kWave), 0, st, a);
       if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
       const int64_t mn = (int64_t)a.M * a.N;
       const unsigned blocks = (unsigned)std::min<int64_t>((mn + kReduceThreads - 1) / kReduceThreads, 4096);
@@ -302,7 +342,7 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
       return EGPT_LAUNCH_STATUS();
     }
   }
-  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false>), dim3(tiles), dim3(kGemmThreads), 0, st, a);
+  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false, WN, NW>), dim3(tiles), dim3(NW * kWave), 0, st, a);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -346,6 +386,10 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
   if (M == 0 || N == 0) return EGPT_OK;
   if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
     return EGPT_ERR_UNSUPPORTED;
+  // the kernel addresses each operand by 32-bit byte offsets
+  if ((int64_t)M * ldx * 2 >= ((int64_t)1 << 31) || (int64_t)N * ldw >= ((int64_t)1 << 31) ||
+      (int64_t)M * ldy * 2 >= ((int64_t)1 << 31))
+    return EGPT_ERR_UNSUPPORTED;
   if (((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX / kMaxSplits) return EGPT_ERR_UNSUPPORTED;
   GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0, 1, K, nullptr};
   if (workspace) {  // a workspace lets short-M shapes split K
@@ -360,10 +404,10 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
       return launch_gemm<64, 64>(a, stream);
     }
   }
-  // The largest tile that still gives every CU a block; small M keeps more, narrower tiles.
-  if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm<256, 256>(a, stream);
-  if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256>(a, stream);
-  if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128>(a, stream);
+// The largest tile that still gives every CU a block; small M keeps more, narrower tiles.
+  if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm<256, 256, kWN256x256, kNW256x256>(a, stream);
+  if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256, kWN256>(a, stream);
+  if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128, kWN128>(a, stream);
   if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
   return launch_gemm<64, 64>(a, stream);
 }
