@@ -57,34 +57,17 @@ struct GemmShape {
 };
 
 // 8 int8 (one LDS fragment) -> 8 bf16, exact.
-#ifndef EGPT_GEMM_CONV
-#define EGPT_GEMM_CONV 0
-#endif
 __device__ __forceinline__ bf16x8 int8x8_to_bf16(const uint32_t w0, const uint32_t w1) {
   const uint32_t w[2] = {w0, w1};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    float f0, f1, f2, f3;
-    if constexpr (EGPT_GEMM_CONV == 1) {
-      f0 = (float)__builtin_amdgcn_sbfe((int)w[i], 0, 8);
-      f1 = (float)__builtin_amdgcn_sbfe((int)w[i], 8, 8);
-      f2 = (float)__builtin_amdgcn_sbfe((int)w[i], 16, 8);
-      f3 = (float)((int)w[i] >> 24);
-    } else if constexpr (EGPT_GEMM_CONV == 2) {
-      const uint32_t u = w[i] ^ 0x80808080u;
-      f0 = (float)(u & 0xffu) - 128.f;
-      f1 = (float)((u >> 8) & 0xffu) - 128.f;
-      f2 = (float)((u >> 16) & 0xffu) - 128.f;
-      f3 = (float)(u >> 24) - 128.f;
-    } else {
-      f0 = (float)(int)(int8_t)(w[i] & 0xffu);
-      f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
-      f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
-      f3 = (float)(int)(int8_t)(w[i] >> 24);
-    }
-    o[2 * i] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-    o[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+    const float f0 = (float)(int)(int8_t)(w[i] & 0xffu);
+    const float f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
+    const float f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
+    const float f3 = (float)(int)(int8_t)(w[i] >> 24);
+    o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+    o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
   }
   return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
@@ -103,9 +86,11 @@ struct GemmArgs {
   float* part;         // splits > 1: fp32 partial tiles [splits][M][N]
 };
 
-// Wavefronts along N of the 128 x 256 and 128 x 128 tiles (the rest of the 4 along M).
+// Wavefronts of the 128 x 256 and 128 x 128 tiles, and how many of them lie along N.
+constexpr int kNW256 = 4;
 constexpr int kWN256 = 4;
-constexpr int kWN128 = 2;
+constexpr int kNW128 = 8;
+constexpr int kWN128 = 4;
 // Wavefronts of the 256 x 256 tile and its wave grid.
 constexpr int kNW256x256 = 8;
 constexpr int kWN256x256 = 4;
@@ -406,8 +391,8 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
   }
 // The largest tile that still gives every CU a block; small M keeps more, narrower tiles.
   if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm<256, 256, kWN256x256, kNW256x256>(a, stream);
-  if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256, kWN256>(a, stream);
-  if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128, kWN128>(a, stream);
+  if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256, kWN256, kNW256>(a, stream);
+  if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128, kWN128, kNW128>(a, stream);
   if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
   return launch_gemm<64, 64>(a, stream);
 }

@@ -240,7 +240,7 @@ def test_small_batch_mfma_kernel_matches_oracle(m, k, n):
 
 PREFILL_SHAPES = [(17, 64, 64), (33, 2048, 4096), (128, 2048, 4096), (100, 2048, 6144), (300, 6144, 2048),
                   (1000, 1024, 96), (257, 4096, 1000), (4096, 2048, 2048), (300, 192, 4096), (4096, 128, 4096),
-                  (2100, 704, 4000), (2304, 320, 7424)]
+                  (2100, 704, 4000), (2304, 320, 7424), (1000, 448, 4100)]
 
 
 @pytest.mark.parametrize('m,k,n', PREFILL_SHAPES)
@@ -248,7 +248,8 @@ def test_prefill_gemm_kernel_matches_oracle(m, k, n):
     """More than 16 rows: the MFMA GEMM (egpt_int8_gemm), against the oracle's prefill formula
     bf16(fp32(bf16(x q^T)) s) and the reference's tolerance; odd N and M exercise the masked edges,
     K = 192 an odd number of 64-wide K steps; 4096 x 2048 -> 2048 and 2100 x 704 -> 4000 (ragged) take the
-    128 x 256 tile, 4096 x 128 -> 4096 and 2304 x 320 -> 7424 (ragged N, 5 K steps) the 8-wavefront 256 x 256 tile."""
+    128 x 256 tile, 4096 x 128 -> 4096 and 2304 x 320 -> 7424 (ragged N, 5 K steps) the 8-wavefront 256 x 256 tile,
+    1000 x 448 -> 4100 the 8-wavefront 128 x 128 tile."""
     from efficientgpt_amd import _lib
     x, q, s = make_case(m, k, n, seed=m + k + n)
     xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
