@@ -59,6 +59,8 @@ SIGNATURES = {
     'egpt_add_rmsnorm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_f, _c_vp]),
     'egpt_qk_norm_rope': (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp,
                                    _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp]),
+    'egpt_prefill_attn': (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int,
+                                   _c_int, _c_int, _c_int, _c_f, _c_vp]),
     'egpt_silu_mul': (_c_int, [_c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_int, _c_vp]),
     'egpt_embed': (_c_int, [_c_vp, _c_int, _c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_int, _c_vp]),
     'egpt_argmax_workspace': (_c_int, [_c_int, ctypes.POINTER(_c_size)]),

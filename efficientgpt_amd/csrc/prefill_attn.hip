@@ -1,0 +1,275 @@
+// Causal GQA attention over a prompt (prefill), flash form on gfx950 MFMA.
+//
+//   out[t, hq, :] = sum_{s <= pos0 + t} softmax_s((q[t, hq] . k[hk, s]) * scale) v[hk, s]
+//
+// for query rows t = 0 .. rows - 1 at positions pos0 + t, query head hq of kv
+// head hk = hq / group. This is the attention of the reference's prompt pass (the
+// transformers Qwen3 forward over the prompt: SDPA with a causal mask over the
+// static cache, HF models/qwen3/modeling_qwen3.py), for which the decode kernels
+// would rescan the prefix once per query row. bf16 q, k, v and output; the logits
+// (q . k) * scale and the online softmax in fp32; the probabilities enter the
+// p . v products as bf16, as in SDPA's bf16 flash path.
+//
+// A block is 4 wavefronts over one kv head; each wavefront owns 32 consecutive
+// query rows of one query head, so a block covers min(group, 4) query heads and
+// 32 * 4 / min(group, 4) positions, and every head of the block shares the K/V
+// tiles it stages. K/V advance 64 slots at a time through two LDS buffers (the
+// global loads of tile j + 1 are issued before tile j is multiplied).
+//
+// Per tile and wavefront, with v_mfma_f32_32x32x16_bf16 (lane l holds A[l % 32]
+// [8 (l / 32) + e] and B[8 (l / 32) + e][l % 32]; accumulator register r of lane
+// l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]):
+//   * S^T = K Q^T: K rows from LDS as A, the wavefront's queries as B (held in
+//     registers for the whole kernel). Lane l's accumulators then hold 16 slots
+//     of ONE query, l % 32 (its other 16 are in lane l ^ 32), so the softmax
+//     statistics of a query are per lane: the row max and sum need one lane swap.
+//   * O^T += V^T P^T: the probabilities go from those accumulators straight into
+//     the B operand (no LDS round trip). That operand's k index 8 (l / 32) + e
+//     then stands for slot 8 (e / 4) + 4 (l / 32) + e % 4 of a 16-slot step
+//     (bits 2 and 3 of the slot swapped), so V^T is staged in LDS with its slots
+//     in that order. The output accumulators also hold one query per lane, so the
+//     online-softmax rescale is per lane too.
+// Padding query rows (past `rows`) read a valid row and are never stored; slots
+// past the block's last position read the last one and are masked.
+#include "common.h"
+
+namespace egpt {
+namespace {
+
+typedef __bf16 bf16x8_pf __attribute__((ext_vector_type(8)));
+typedef float f32x16_pf __attribute__((ext_vector_type(16)));
+
+constexpr int kPfD = 128;              // head dim
+constexpr int kPfSlots = 64;           // K/V slots per tile
+constexpr int kPfThreads = 256;        // 4 wavefronts
+constexpr int kPfKRow = kPfD + 8;      // bf16 per K row in LDS (16 bytes of padding)
+constexpr int kPfVRow = kPfSlots + 8;  // bf16 per V^T row in LDS
+constexpr float kPfLog2e = 1.4426950408889634f;
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t q_ld;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t c_sh, c_sn;
+  uint16_t* out;
+  int64_t o_ld;
+  int rows, group, pos0;
+  int hb;      // query heads per block
+  int bt;      // query positions per block
+  int ntiles;  // position tiles
+  float scale;
+};
+
+// Position of slot s (0..15 of a 16-slot step) in the staged V^T row: bits 2 and 3 swapped.
+__device__ __forceinline__ int vperm(int s) { return (s & 3) | ((s >> 2 & 1) << 3) | ((s >> 3 & 1) << 2); }
+
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_attn_kernel(const PrefillArgs a) {
+  __shared__ __align__(16) uint16_t Ks[2][kPfSlots * kPfKRow];
+  __shared__ __align__(16) uint16_t Vs[2][kPfD * kPfVRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  // Block -> (kv head, subset of its query heads, position tile). The first
+  // blocks dispatched take the last position tiles, whose causal ranges are the
+  // longest.
+  const int subsets = a.group / a.hb;
+  const int hk = (int)blockIdx.x / subsets;
+  const int sub = (int)blockIdx.x % subsets;
+  const int ptile = a.ntiles - 1 - (int)blockIdx.y;
+  const int t0 = ptile * a.bt;
+  const int wph = a.bt / 32;  // wavefronts per query head
+  const int hq = hk * a.group + sub * a.hb + wave / wph;
+  const int tw = t0 + (wave % wph) * 32;  // the wavefront's first query row
+  const int tq = tw + col;                // this lane's query row
+  const int64_t qpos = (int64_t)a.pos0 + tq;
+  // Slots this block visits: 0 .. its last query's position.
+  const int64_t last = (int64_t)a.pos0 + min(t0 + a.bt, a.rows) - 1;
+  const int nt = (int)(last / kPfSlots) + 1;
+
+  // B fragments of Q^T: this lane's query, dims 16 kk + 8 half .. + 7.
+  u32x4 qf[kPfD / 16];
+  {
+    const uint16_t* qrow = a.q + (int64_t)min(tq, a.rows - 1) * a.q_ld + (int64_t)hq * kPfD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < kPfD / 16; ++kk) qf[kk] = ld16(qrow + 16 * kk);
+  }
+
+  // Staging of one K/V tile: 64 slots x 16 chunks of 8 dims each for K and V. A
+  // thread takes K chunks (slot c / 16, chunk c % 16) for c = tid + 256 i, and V
+  // chunk `vc` of the four consecutive slots 4 vg .. 4 vg + 3, whose staged
+  // positions are consecutive too (vperm keeps bits 0 and 1), so each of its 8
+  // dims is one 8-byte LDS store.
+  const uint16_t* kb = a.k + (int64_t)hk * a.c_sh;
+  const uint16_t* vb = a.v + (int64_t)hk * a.c_sh;
+  const int vg = tid / 16, vc = tid % 16;
+  u32x4 kr[4], vr[4];
+  auto gload = [&](int j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kPfThreads * i;
+      const int64_t s = min((int64_t)j * kPfSlots + c / 16, last);
+      kr[i] = ld16(kb + s * a.c_sn + (c % 16) * 8);
+      const int64_t sv = min((int64_t)j * kPfSlots + 4 * vg + i, last);
+      vr[i] = ld16(vb + sv * a.c_sn + vc * 8);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kPfThreads * i;
+      *(u32x4*)&Ks[buf][(c / 16) * kPfKRow + (c % 16) * 8] = kr[i];
+    }
+    // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions
+    const int p0 = (4 * vg) & ~15;
+    const int p = p0 + vperm((4 * vg) & 15);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = 16 * (e & 1);
+      const uint32_t w0 = ((e < 2 ? vr[0].x : e < 4 ? vr[0].y : e < 6 ? vr[0].z : vr[0].w) >> sh) & 0xffffu;
+      const uint32_t w1 = ((e < 2 ? vr[1].x : e < 4 ? vr[1].y : e < 6 ? vr[1].z : vr[1].w) >> sh) & 0xffffu;
+      const uint32_t w2 = ((e < 2 ? vr[2].x : e < 4 ? vr[2].y : e < 6 ? vr[2].z : vr[2].w) >> sh) & 0xffffu;
+      const uint32_t w3 = ((e < 2 ? vr[3].x : e < 4 ? vr[3].y : e < 6 ? vr[3].z : vr[3].w) >> sh) & 0xffffu;
+      *(uint2*)&Vs[buf][(vc * 8 + e) * kPfVRow + p] = make_uint2(w0 | (w1 << 16), w2 | (w3 << 16));
+    }
+  };
+
+  f32x16_pf o[kPfD / 32];
+#pragma unroll
+  for (int dt = 0; dt < kPfD / 32; ++dt) o[dt] = f32x16_pf{};
+  float m = -INFINITY, l = 0.f;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+#pragma unroll 1
+  for (int j = 0; j < nt; ++j) {
+    const int buf = j & 1;
+    if (j + 1 < nt) gload(j + 1);
+    // S^T for slots 64 j + 32 mt + (8 (r / 4) + 4 half + r % 4), query col
+    f32x16_pf st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      st[mt] = f32x16_pf{};
+      const uint16_t* kr0 = &Ks[buf][(32 * mt + col) * kPfKRow + 8 * half];
+#pragma unroll
+      for (int kk = 0; kk < kPfD / 16; ++kk) {
+        const u32x4 av = *(const u32x4*)(kr0 + 16 * kk);
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
+                                                         __builtin_bit_cast(bf16x8_pf, qf[kk]), st[mt], 0, 0, 0);
+      }
+    }
+    // Online softmax of this lane's query over the tile's 64 slots (32 here, 32 in lane ^ 32).
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t slot = (int64_t)j * kPfSlots + 32 * mt + 8 * (r / 4) + 4 * half + r % 4;
+        const float sv = slot <= qpos ? st[mt][r] * a.scale : -INFINITY;  // the fp32 logit (q . k) * scale
+        st[mt][r] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    LanePair pr = pair32(mx);
+    mx = fmaxf(pr.lo, pr.hi);
+    const float mn = fmaxf(m, mx);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f((m - mref) * kPfLog2e);
+    float ps = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f((st[mt][r] - mref) * kPfLog2e);  // 0 for masked slots
+        st[mt][r] = p;
+        ps += p;
+      }
+    pr = pair32(ps);
+    ps = pr.lo + pr.hi;
+    l = l * alpha + ps;
+    m = mn;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // once the maxima settle alpha is exactly 1
+#pragma unroll
+      for (int dt = 0; dt < kPfD / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
+    // O^T += V^T P^T over the four 16-slot steps of the tile.
+#pragma unroll
+    for (int js = 0; js < 4; ++js) {
+      const f32x16_pf& pt = st[js / 2];
+      uint32_t pk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pk[e] = (uint32_t)f32_to_bf16(pt[8 * (js % 2) + 2 * e]) |
+                ((uint32_t)f32_to_bf16(pt[8 * (js % 2) + 2 * e + 1]) << 16);
+      const bf16x8_pf pb = __builtin_bit_cast(bf16x8_pf, u32x4{pk[0], pk[1], pk[2], pk[3]});
+      const uint16_t* vr0 = &Vs[buf][col * kPfVRow + 16 * js + 8 * half];
+#pragma unroll
+      for (int dt = 0; dt < kPfD / 32; ++dt) {
+        const u32x4 av = *(const u32x4*)(vr0 + 32 * dt * kPfVRow);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av), pb, o[dt], 0, 0, 0);
+      }
+    }
+    if (j + 1 < nt) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // out[tq, hq, 32 dt + 8 (r / 4) + 4 half + r % 4] = o / l, four dims per 8-byte store
+  if (tq < a.rows) {
+    const float inv = 1.f / l;
+    uint16_t* orow = a.out + (int64_t)tq * a.o_ld + (int64_t)hq * kPfD + 4 * half;
+#pragma unroll
+    for (int dt = 0; dt < kPfD / 32; ++dt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const uint32_t lo = (uint32_t)f32_to_bf16(o[dt][4 * r4] * inv) |
+                            ((uint32_t)f32_to_bf16(o[dt][4 * r4 + 1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(o[dt][4 * r4 + 2] * inv) |
+                            ((uint32_t)f32_to_bf16(o[dt][4 * r4 + 3] * inv) << 16);
+        *(uint2*)(orow + 32 * dt + 8 * r4) = make_uint2(lo, hi);
+      }
+  }
+}
+
+}  // namespace
+}  // namespace egpt
+
+using namespace egpt;
+
+extern "C" int egpt_prefill_attn(const void* q, int64_t q_ld, const void* k, const void* v, int64_t c_sh,
+                                 int64_t c_sn, void* out, int64_t o_ld, int rows, int Hq, int Hkv, int D, int cap,
+                                 int pos0, float scale, hipStream_t stream) {
+  if (!q || !k || !v || !out || rows < 0 || Hq < 1 || Hkv < 1 || Hq % Hkv || cap < 1 || pos0 < 0) return EGPT_ERR_INVALID;
+  if (rows == 0) return EGPT_OK;
+  if ((int64_t)pos0 + rows > cap) return EGPT_ERR_INVALID;
+  if (D != kPfD) return EGPT_ERR_UNSUPPORTED;
+  const int group = Hq / Hkv;
+  if (group != 1 && group != 2 && group != 4 && group != 8) return EGPT_ERR_UNSUPPORTED;
+  if (q_ld < (int64_t)Hq * D || o_ld < (int64_t)Hq * D || c_sn < D || c_sh < (int64_t)cap * c_sn) return EGPT_ERR_INVALID;
+  if (q_ld % 8 || o_ld % 4 || c_sn % 8 || c_sh % 8 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 ||
+      (uintptr_t)out % 8)
+    return EGPT_ERR_UNSUPPORTED;
+  PrefillArgs a{};
+  a.q = (const uint16_t*)q;
+  a.q_ld = q_ld;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.c_sh = c_sh;
+  a.c_sn = c_sn;
+  a.out = (uint16_t*)out;
+  a.o_ld = o_ld;
+  a.rows = rows;
+  a.group = group;
+  a.pos0 = pos0;
+  a.hb = group < 4 ? group : 4;
+  a.bt = 32 * 4 / a.hb;
+  a.ntiles = (rows + a.bt - 1) / a.bt;
+  a.scale = scale;
+  const dim3 grid((unsigned)(Hkv * (group / a.hb)), (unsigned)a.ntiles);
+  hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kPfThreads), 0, stream, a);
+  return EGPT_LAUNCH_STATUS();
+}

@@ -25,7 +25,8 @@ Step (token t at position p; writes K/V slot p, attends to slots 0..p):
   down GEMV -> ... -> add+final RMSNorm -> lm_head GEMV -> argmax (token, p + 1).
 Prefill runs the same kernels over all prompt rows, outside the graph; linears past 16
 rows take the reference's prefill formula (int8_linear.py:96-97) on the MFMA GEMM that
-reads the int8 weights, and on the library GEMM past its row limit.
+reads the int8 weights, and prompts past PREFILL_KERNEL_MAX_ROWS rows the causal MFMA
+prefill attention (egpt_prefill_attn).
 """
 
 import ctypes
@@ -36,7 +37,8 @@ import torch
 from . import _lib
 from .int8_linear import MAX_DECODE_ROWS, int8_gemm, quantize_weight
 
-# Prompts longer than this take the library-GEMM attention in prefill.
+# Prompts longer than this take the causal prefill attention (egpt_prefill_attn; the library-GEMM form for head
+# dims it does not take) instead of the split-K decode kernel, which would rescan the prefix once per query row.
 PREFILL_KERNEL_MAX_ROWS = 64
 
 LINEARS = ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj', 'self_attn.o_proj',
@@ -354,7 +356,13 @@ class Qwen3Int8Engine:
             self.cos.data_ptr(), self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(),
             kc.stride(0), kc.stride(1), rows, c.heads, c.kv_heads, d, self.cap, c.rms_eps, st))
         if rows > PREFILL_KERNEL_MAX_ROWS:
-            self._prefill_attention(qrot, kc, vc, rows, pos0, attn)
+            st_pf = lib.egpt_prefill_attn(qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(), kc.stride(0),
+                                          kc.stride(1), attn.data_ptr(), attn.stride(0), rows, c.heads, c.kv_heads, d,
+                                          self.cap, pos0, d ** -0.5, st)
+            if st_pf == _lib.EGPT_ERR_UNSUPPORTED:  # head dim other than 128
+                self._prefill_attention(qrot, kc, vc, rows, pos0, attn)
+            else:
+                _lib.check('egpt_prefill_attn', st_pf)
         else:
             self._kernel_attention(qrot, kc, vc, rows, positions, pos_stride, attn)
         self._linear(attn, L['o_q'], L['o_s'], o, rows)

@@ -173,6 +173,21 @@ int egpt_qk_norm_rope(const void *qkv, int64_t ld_qkv, const int64_t *positions,
                       void *k_cache, void *v_cache, int64_t cache_head_stride, int64_t cache_slot_stride,
                       int rows, int Hq, int Hkv, int D, int cap, float eps, hipStream_t stream);
 
+/* Causal attention of a prompt block: query row t (position pos0 + t, head hq of
+ * kv head hq / (Hq / Hkv)) attends cache slots 0 .. pos0 + t,
+ *   out[t, hq] = softmax((q[t, hq] . k[s]) * scale) v,
+ * the prompt pass of the reference's Qwen3 path (Qwen3Attention.forward over the
+ * prompt: SDPA with the causal mask over the static cache, modeling_qwen3.py:252-280,
+ * integrations/sdpa_attention.py:79-102). bf16 q [rows, Hq*D] (row stride q_ld, the
+ * rotated queries of egpt_qk_norm_rope), caches [Hkv, cap, D] (strides cache_head_stride,
+ * cache_slot_stride) already holding slots 0 .. pos0 + rows - 1, bf16 out [rows, Hq*D]
+ * (row stride o_ld). fp32 logits and softmax; the probabilities multiply v as bf16.
+ * D 128, Hq / Hkv in {1, 2, 4, 8} (else EGPT_ERR_UNSUPPORTED: the caller keeps its
+ * library attention). */
+int egpt_prefill_attn(const void *q, int64_t q_ld, const void *k_cache, const void *v_cache,
+                      int64_t cache_head_stride, int64_t cache_slot_stride, void *out, int64_t o_ld, int rows,
+                      int Hq, int Hkv, int D, int cap, int pos0, float scale, hipStream_t stream);
+
 /* act = bf16(bf16(silu(gate)) * up) over rows laid out [gate (inter) | up (inter)]
  * (Qwen3MLP, modeling_qwen3.py:49-62). */
 int egpt_silu_mul(const void *gu, int64_t ld_gu, int inter, void *out, int64_t ld_out, int rows,

@@ -6,6 +6,8 @@
   attention_splitk     fp32 restatement of the reference's flash-decoding pair:
                        _split_kernel (research/phase5/decode_attention.py:31-56) per split of
                        SPLIT slots in BLOCK_N tiles, then _combine_kernel (:59-71).
+  prefill_truth        fp64 causal attention of a prompt block (query row t at position pos0 + t)
+                       over a static cache, the prompt pass of transformers' Qwen3 attention.
   bytes_moved          algorithmic bytes of one call (K and V rows read once, q read, out written).
 Inputs are numpy arrays: q [B, Hq, 1, D], k/v [B, Hkv, cap, D], position int64 [1] or [B].
 """
@@ -72,6 +74,29 @@ def attention_splitk(q, k, v, position, split=16, block_n=16):
                 ms[s_idx], ls[s_idx], accs[s_idx] = m_i, l_i, acc
             w = np.exp(ms - ms.max()).astype(f32)  # empty splits: m = -inf -> weight 0
             out[b, h, 0] = (accs * w[:, None]).sum(0, dtype=f32) / (ls * w).sum(dtype=f32)
+    return out
+
+
+def prefill_truth(q, k, v, pos0, scale=None):
+    """fp64 causal attention of a prompt block over a static cache (the prompt pass of transformers'
+    Qwen3Attention.forward: SDPA with the causal mask over the cache, HF models/qwen3/modeling_qwen3.py:252-280,
+    integrations/sdpa_attention.py:79-102). q [rows, Hq, D] holds query rows at positions pos0 + t; k, v
+    [Hkv, cap, D]; row t of query head h attends slots 0 .. pos0 + t of kv head h // G. Returns [rows, Hq, D]."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    rows, hq, d = q.shape
+    hkv = k.shape[0]
+    g = hq // hkv
+    scale = d ** -0.5 if scale is None else scale
+    n = pos0 + rows
+    allowed = np.arange(n)[None, :] <= (pos0 + np.arange(rows))[:, None]  # [rows, n]
+    out = np.zeros((rows, hq, d))
+    for h in range(hq):
+        s = (q[:, h] @ k[h // g, :n].T) * scale
+        s = np.where(allowed, s, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ v[h // g, :n]
     return out
 
 

@@ -170,6 +170,28 @@ def test_attention_mask_off_by_one_is_caught():
     assert np.abs(wrong - truth).max() > 1e-3
 
 
+def test_prefill_truth_rows_equal_decode_attention_and_causal_sdpa():
+    # row t of a prompt block at pos0 is the decode attention at position pos0 + t over the same cache
+    rng = np.random.default_rng(8)
+    hq, hkv, cap, d, pos0, rows = 8, 2, 50, 32, 13, 29
+    q = rng.standard_normal((rows, hq, d)) * 2.0
+    k = rng.standard_normal((hkv, cap, d)) * 2.0
+    v = rng.standard_normal((hkv, cap, d))
+    got = oatt.prefill_truth(q, k, v, pos0)
+    per_row = oatt.attention_truth(q[:, :, None, :], np.repeat(k[None], rows, 0), np.repeat(v[None], rows, 0),
+                                   pos0 + np.arange(rows))
+    assert np.allclose(got, per_row[:, :, 0], atol=1e-12, rtol=0)
+    # from position 0 over exactly `rows` slots it is torch's causal SDPA (is_causal), repeat_kv applied
+    got0 = oatt.prefill_truth(q, k, v, 0)
+    tq = torch.from_numpy(q).permute(1, 0, 2)
+    tk = torch.from_numpy(np.repeat(k[:, :rows], hq // hkv, 0))
+    tv = torch.from_numpy(np.repeat(v[:, :rows], hq // hkv, 0))
+    sdpa = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True).permute(1, 0, 2).numpy()
+    assert np.allclose(got0, sdpa, atol=1e-12, rtol=0)
+    # the mask shifted by one slot (each row also seeing the next slot) is caught
+    assert np.abs(oatt.prefill_truth(q, k, v, pos0 + 1) - got).max() > 1e-3
+
+
 # ---------------------------------------------------------------- Qwen3 step vs transformers
 
 def _fp32_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
