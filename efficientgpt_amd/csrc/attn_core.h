@@ -24,15 +24,6 @@ namespace egpt {
 constexpr int kAttnThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Workgroup barrier ordering LDS only. __syncthreads() also waits for every
-// outstanding global load of the wavefront (s_waitcnt vmcnt(0)), which would
-// stall the block behind loads still in flight at each LDS hand-off.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Geometry of one attention block of NT threads over rows of D elements of T:
 // a lane issues LPR 16-byte loads per K (and V) row, so it owns EPL contiguous
 // elements; LPS lanes cover a row; the block runs NG independent softmax

@@ -90,6 +90,15 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load((global_ptr<const u32x4>)p);
 }
 
+// Workgroup barrier ordering LDS only. __syncthreads() also waits for every
+// outstanding global load of the wavefront (s_waitcnt vmcnt(0)), which would
+// stall the block behind loads still in flight at each LDS hand-off.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------- DPP reductions
 
 template <int CTRL>

@@ -264,12 +264,156 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma(
   }
 }
 
+// The same contraction for wide outputs with short rows (K <= 64 * 8 * SPW): a
+// capped grid whose blocks walk tiles of FG groups of 16 features. As in
+// gemv_i8_mfma<8, FG>, the 8 wavefronts of a block split K (wavefront j takes
+// the 64-wide steps j, j + 8, ...) and their tiles are summed through LDS in
+// wavefront order, so the outputs are bit-identical to it. What differs: each
+// wavefront loads its activation fragments once and keeps them in registers,
+// and the next tile's weights (and scales) are issued before this tile is
+// multiplied, in two fixed register buffers, so a block keeps streaming while it
+// reduces instead of ending after one short burst of loads. Loads past the last
+// tile re-read the block's own tile (unconditional loads keep the wait counts
+// exact). The LDS tiles alternate between two buffers: one barrier per tile.
+template <int SPW, int FG>
+struct MfmaTile {
+  u32x4 w[SPW][FG];
+  float sc[(FG * 256 + kMfmaWaves * kWave - 1) / (kMfmaWaves * kWave)];
+};
+
+template <int SPW, int FG>
+__device__ __forceinline__ void mfma_tile_load(MfmaTile<SPW, FG>& b, const int8_t* __restrict__ w, int64_t ldw,
+                                               const float* __restrict__ scale, int N, int64_t tile, int steps,
+                                               int lane, int wave) {
+  constexpr int kE = (FG * 256 + kMfmaWaves * kWave - 1) / (kMfmaWaves * kWave);
+  const int64_t n0 = tile * 16 * FG;
+#pragma unroll
+  for (int i = 0; i < kE; ++i) {
+    const int e = min((int)threadIdx.x + i * kMfmaWaves * kWave, FG * 256 - 1);
+    b.sc[i] = scale[min(n0 + 16 * (e / 256) + (e % 256) % 16, (int64_t)N - 1)];
+  }
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const int st = min(wave + kMfmaWaves * j, steps - 1);
+#pragma unroll
+    for (int f = 0; f < FG; ++f)
+      b.w[j][f] = ld16_stream(w + min(n0 + 16 * f + lane % 16, (int64_t)N - 1) * ldw + 16 * (lane / 16) + st * 64);
+  }
+}
+
+template <int SPW, int FG>
+__device__ __forceinline__ void mfma_tile_finish(const MfmaTile<SPW, FG>& b, const u32x4 (&xa)[SPW],
+                                                 const u32x4 (&xb)[SPW], float* red, uint16_t* __restrict__ y,
+                                                 int64_t ldy, int m_rows, int N, int64_t tile, int steps, int lane,
+                                                 int wave) {
+  f32x4_t acc[FG];
+#pragma unroll
+  for (int f = 0; f < FG; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    if (wave + kMfmaWaves * j < steps) {
+#pragma unroll
+      for (int f = 0; f < FG; ++f) {
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[j]),
+                                                         int8x8_bf16(b.w[j][f].x, b.w[j][f].y), acc[f], 0, 0, 0);
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xb[j]),
+                                                         int8x8_bf16(b.w[j][f].z, b.w[j][f].w), acc[f], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < FG; ++f)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave * FG * 256 + f * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = acc[f][r];
+  lds_barrier();
+  constexpr int kE = (FG * 256 + kMfmaWaves * kWave - 1) / (kMfmaWaves * kWave);
+#pragma unroll
+  for (int i = 0; i < kE; ++i) {
+    const int e = (int)threadIdx.x + i * kMfmaWaves * kWave;
+    if (e < FG * 256) {
+      float sum = red[e];
+#pragma unroll
+      for (int j = 1; j < kMfmaWaves; ++j) sum += red[j * FG * 256 + e];
+      const int m = (e % 256) / 16;
+      const int64_t nn = tile * 16 * FG + 16 * (e / 256) + (e % 256) % 16;
+      if (m < m_rows && nn < N) y[(int64_t)m * ldy + nn] = f32_to_bf16(sum * b.sc[i]);
+    }
+  }
+}
+
+template <int SPW, int FG>
+__global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma_walk(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, uint16_t* __restrict__ y, int64_t ldy, int m_rows, int N, int K) {
+  __shared__ float red[2][kMfmaWaves * FG * 256];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int steps = K / 64;
+  const int64_t ntiles = ((int64_t)N + 16 * FG - 1) / (16 * FG);
+  const int64_t stride = gridDim.x;
+  // activation fragments of this wavefront's K steps (a step past the end is a
+  // valid one, never accumulated)
+  const uint16_t* xrow = x + (int64_t)min(lane % 16, m_rows - 1) * ldx + 16 * (lane / 16);
+  u32x4 xa[SPW], xb[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const int st = min(wave + kMfmaWaves * j, steps - 1);
+    xa[j] = ld16(xrow + st * 64);
+    xb[j] = ld16(xrow + st * 64 + 8);
+  }
+  int64_t t = blockIdx.x;
+  MfmaTile<SPW, FG> ta, tb;
+  mfma_tile_load<SPW, FG>(ta, w, ldw, scale, N, t, steps, lane, wave);
+#pragma unroll 1
+  for (;;) {
+    const int64_t u = t + stride;
+    mfma_tile_load<SPW, FG>(tb, w, ldw, scale, N, u < ntiles ? u : t, steps, lane, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tile_finish<SPW, FG>(ta, xa, xb, red[0], y, ldy, m_rows, N, t, steps, lane, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    if (u >= ntiles) break;
+    const int64_t v = u + stride;
+    mfma_tile_load<SPW, FG>(ta, w, ldw, scale, N, v < ntiles ? v : u, steps, lane, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_tile_finish<SPW, FG>(tb, xa, xb, red[1], y, ldy, m_rows, N, u, steps, lane, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    if (v >= ntiles) break;
+    t = v;
+  }
+}
+
 template <int G, int FG>
 void launch_mfma(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
                  int64_t ldy, int M, int N, int K, hipStream_t st) {
   const int64_t per_block = 16 * FG * (kMfmaWaves / G);
   hipLaunchKernelGGL((gemv_i8_mfma<G, FG>), dim3((unsigned)((N + per_block - 1) / per_block)),
                      dim3(kMfmaWaves * kWave), 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K);
+}
+
+// Blocks of the tile-walking MFMA GEMV: one per CU (512 and 1024 measured
+// slower: 10-30% at 151936 x 2048, 12288 x 2048 and 70001 x 1024).
+constexpr int kMfmaWalkBlocks = 256;
+// It takes outputs wider than this with rows of at most 2048 (K / 64 steps over
+// 8 wavefronts, at most 4 each). Against gemv_i8_mfma (A/B on one box, cold,
+// 3-16 rows): 151936 x 2048 72-78 -> 70-76 us, 12288 x 2048 9.1-11.5 ->
+// 8.7-9.4, 70001 x 1024 30-35 -> 20-22; at 8192 and 4096 features, with two and
+// one tiles per block, it is no faster.
+constexpr int64_t kMfmaWalkMinN = 8192;
+
+template <int FG>
+int launch_mfma_walk(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
+                     int64_t ldy, int M, int N, int K, hipStream_t st) {
+  const int spw = (K / 64 + kMfmaWaves - 1) / kMfmaWaves;
+  const int64_t tiles = ((int64_t)N + 16 * FG - 1) / (16 * FG);
+  const dim3 grid((unsigned)(tiles < kMfmaWalkBlocks ? tiles : kMfmaWalkBlocks)), block(kMfmaWaves * kWave);
+  switch (spw) {
+    case 1: hipLaunchKernelGGL((gemv_i8_mfma_walk<1, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 2: hipLaunchKernelGGL((gemv_i8_mfma_walk<2, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 3:
+    case 4: hipLaunchKernelGGL((gemv_i8_mfma_walk<4, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    default: return EGPT_ERR_UNSUPPORTED;
+  }
+  return EGPT_LAUNCH_STATUS();
 }
 
 // Feature groups per MFMA wavefront: four for outputs of at least this many
@@ -420,6 +564,10 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
     // all 8 wavefronts on one 16-feature group: splitting K eight ways keeps the most
     // loads in flight (measured faster than 1, 2 or 4 wavefronts per group at every
     // Qwen3-1.7B shape, the 151936-row lm_head included)
+    if (K <= 64 * kMfmaWaves * 4 && N > kMfmaWalkMinN) {
+      if (N >= kMfmaWideN) return launch_mfma_walk<4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+      return launch_mfma_walk<1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+    }
     if (N >= kMfmaWideN) launch_mfma<kMfmaWaves, 4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
     else launch_mfma<kMfmaWaves, 1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
     return EGPT_LAUNCH_STATUS();
