@@ -382,6 +382,153 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma_walk(
   }
 }
 
+// LDS-staged form of the walking GEMV, for K a multiple of 512 up to 2048. The
+// MFMA operand layout puts 16 weight rows in every load instruction (64 bytes
+// of each): streamed that way an int8 matrix moves at 4.2 TB/s on the MI355X,
+// against 6.4 TB/s for loads that cover 1 KiB of consecutive bytes (a stream
+// of 151936 x 2048, measured). Here the weights go straight from memory into
+// LDS (global_load_lds_dwordx4: lane i of a load writes LDS bytes 16 i .. 16 i
+// + 15 from the base in M0, checked on the MI355X), each load covering two
+// 512-byte row slices, and the MFMA fragments are read from LDS. A tile of FG
+// groups of 16 features is streamed in chunks of 512 K bytes; wavefront j
+// loads rows 2 FG j .. 2 FG j + 2 FG - 1 of each chunk and multiplies the
+// chunk's step j (K 64 j .. 64 j + 63), so over a tile it takes the steps j,
+// j + 8, ... in order, as gemv_i8_mfma_walk does, with the same MFMAs and the
+// same wavefront-order reduction: the outputs are bit-identical to it. The
+// tile's scales come into LDS the same way. Three chunk buffers: the loads of
+// chunk q + 2 are issued once every wavefront has passed chunk q's barrier (so
+// none still reads that buffer), and each wait covers one chunk. In LDS a row's
+// 16-byte unit u sits at unit u ^ (row % 16), so the 16 rows a fragment read
+// touches fall on distinct banks.
+//
+// The LDS loads are issued from inline assembly, and the kernel waits for them
+// itself (s_waitcnt vmcnt counts every vector memory operation in issue order):
+// the compiler, seeing them, waits for all of them before any LDS read.
+constexpr int kLdsChunk = 512;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+__device__ __forceinline__ void lds_load16(uint32_t lds_base, const void* g) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void lds_load4(uint32_t lds_base, const void* g) {
+  asm volatile("global_load_lds_dword %0, off" : : "v"(g), "{m0}"(lds_base) : "memory");
+}
+// s_waitcnt vmcnt(n) with the other counters left alone.
+#define EGPT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+template <int FG>
+__device__ __forceinline__ void lds_chunk_issue(int8_t* buf, const int8_t* __restrict__ w, int64_t ldw, int N,
+                                                int64_t tile, int c, int lane, int wave) {
+#pragma unroll
+  for (int i = 0; i < FG; ++i) {
+    const int r = 2 * FG * wave + 2 * i + lane / 32;  // row within the tile
+    const int64_t row = min(tile * 16 * FG + r, (int64_t)N - 1);
+    const int u = (lane % 32) ^ (r % 16);  // the unit this lane's LDS slot holds
+    lds_load16(lds_addr(buf + (2 * FG * wave + 2 * i) * kLdsChunk), w + row * ldw + c * kLdsChunk + 16 * u);
+  }
+}
+
+template <int SPW, int FG>
+__global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma_lds(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, uint16_t* __restrict__ y, int64_t ldy, int m_rows, int N, int K) {
+  constexpr int kE = (FG * 256 + kMfmaWaves * kWave - 1) / (kMfmaWaves * kWave);
+  constexpr int kBuf = 16 * FG * kLdsChunk;
+  __shared__ __align__(16) int8_t wsm[3 * kBuf];
+  __shared__ float red[kMfmaWaves * FG * 256];
+  __shared__ float scs[3][kWave];  // the scales of a tile (16 FG used): slot = the block's tile index % 3
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t ntiles = ((int64_t)N + 16 * FG - 1) / (16 * FG);
+  const int64_t stride = gridDim.x;
+  // activation fragments of this wavefront's steps j + 8 c (all inside K = 512 SPW),
+  // complete before the first weight load goes out
+  const uint16_t* xrow = x + (int64_t)min(lane % 16, m_rows - 1) * ldx + 16 * (lane / 16);
+  u32x4 xa[SPW], xb[SPW];
+#pragma unroll
+  for (int c = 0; c < SPW; ++c) {
+    xa[c] = ld16(xrow + (wave + kMfmaWaves * c) * 64);
+    xb[c] = ld16(xrow + (wave + kMfmaWaves * c) * 64 + 8);
+  }
+  // (the empty asm takes the fragments as inputs, so the compiler waits for them
+  // here rather than moving the loads below the first weight loads)
+#pragma unroll
+  for (int c = 0; c < SPW; ++c) asm volatile("" : : "v"(xa[c]), "v"(xb[c]) : "memory");
+  // Chunk position p: tile t0 + (p / SPW) stride, chunk p % SPW, buffer p % 3; a
+  // position past the last tile re-reads that chunk of the block's first tile. A
+  // tile's scales go out just before its first chunk, two tiles ahead at most.
+  auto issue = [&](int64_t p) {
+    int64_t tile = (int64_t)blockIdx.x + (p / SPW) * stride;
+    const int c = (int)(p % SPW);
+    if (tile >= ntiles) tile = blockIdx.x;
+    if (c == 0)
+      lds_load4(lds_addr(scs[(p / SPW) % 3]), scale + min(tile * 16 * FG + lane, (int64_t)N - 1));
+    lds_chunk_issue<FG>(wsm + (int)(p % 3) * kBuf, w, ldw, N, tile, c, lane, wave);
+  };
+  issue(0);
+  issue(1);
+  int64_t p = 0;
+  int slot = 0;
+  f32x4_t acc[FG];
+#pragma unroll 1
+  for (int64_t t = blockIdx.x; t < ntiles; t += stride, slot = slot == 2 ? 0 : slot + 1) {
+#pragma unroll
+    for (int c = 0; c < SPW; ++c) {
+      // Chunk p is in once no more than the operations issued after it are
+      // outstanding: chunk p + 1 (FG loads), preceded by its tile's scales when
+      // it starts one, and any stores since (more waiting, never less).
+      __builtin_amdgcn_sched_barrier(0);
+      if (c == SPW - 1) {
+        EGPT_WAIT_VMCNT(FG + 1);
+      } else {
+        EGPT_WAIT_VMCNT(FG);
+      }
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // chunk p + 2 goes into the buffer chunk p - 1 used: every wavefront is past it
+      issue(p + 2);
+      if (c == 0) {
+#pragma unroll
+        for (int f = 0; f < FG; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      const int8_t* buf = wsm + (int)(p % 3) * kBuf;
+#pragma unroll
+      for (int f = 0; f < FG; ++f) {
+        const int r = 16 * f + lane % 16;
+        const int u = (4 * wave + lane / 16) ^ (r % 16);
+        const u32x4 fr = *(const u32x4*)(buf + r * kLdsChunk + 16 * u);
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[c]),
+                                                         int8x8_bf16(fr.x, fr.y), acc[f], 0, 0, 0);
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xb[c]),
+                                                         int8x8_bf16(fr.z, fr.w), acc[f], 0, 0, 0);
+      }
+      ++p;
+    }
+    // wavefront-order reduction of the tile, scale, store (the chunk barriers of
+    // the next tile separate these reads from its writes)
+#pragma unroll
+    for (int f = 0; f < FG; ++f)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave * FG * 256 + f * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = acc[f][r];
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < kE; ++i) {
+      const int e = (int)threadIdx.x + i * kMfmaWaves * kWave;
+      if (e < FG * 256) {
+        float sum = red[e];
+#pragma unroll
+        for (int j = 1; j < kMfmaWaves; ++j) sum += red[j * FG * 256 + e];
+        const int m = (e % 256) / 16;
+        const int fi = 16 * (e / 256) + (e % 256) % 16;
+        const int64_t nn = t * 16 * FG + fi;
+        if (m < m_rows && nn < N) y[(int64_t)m * ldy + nn] = f32_to_bf16(sum * scs[slot][fi]);
+      }
+    }
+  }
+}
+
 template <int G, int FG>
 void launch_mfma(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
                  int64_t ldy, int M, int N, int K, hipStream_t st) {
@@ -411,6 +558,28 @@ int launch_mfma_walk(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ld
     case 2: hipLaunchKernelGGL((gemv_i8_mfma_walk<2, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
     case 3:
     case 4: hipLaunchKernelGGL((gemv_i8_mfma_walk<4, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    default: return EGPT_ERR_UNSUPPORTED;
+  }
+  return EGPT_LAUNCH_STATUS();
+}
+
+// Blocks of the LDS-staged GEMV: one per CU with four feature groups per tile
+// (128.5 KiB of LDS), two with one. Measured against 512 / 256 (A/B on one box,
+// cold, 3-16 rows): 151936 x 2048 56-60 against 57-61 us, 12288 x 2048 8.1-9.7
+// against 9.2-10.1, 20000 x 1536 9.2-10.6 against 11.6-12.5.
+template <int FG>
+constexpr unsigned mfma_lds_blocks() { return FG == 4 ? 256 : 512; }
+
+template <int FG>
+int launch_mfma_lds(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
+                    int64_t ldy, int M, int N, int K, hipStream_t st) {
+  const int64_t tiles = ((int64_t)N + 16 * FG - 1) / (16 * FG);
+  const dim3 grid((unsigned)(tiles < mfma_lds_blocks<FG>() ? tiles : mfma_lds_blocks<FG>())), block(kMfmaWaves * kWave);
+  switch (K / kLdsChunk) {
+    case 1: hipLaunchKernelGGL((gemv_i8_mfma_lds<1, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 2: hipLaunchKernelGGL((gemv_i8_mfma_lds<2, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 3: hipLaunchKernelGGL((gemv_i8_mfma_lds<3, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 4: hipLaunchKernelGGL((gemv_i8_mfma_lds<4, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
     default: return EGPT_ERR_UNSUPPORTED;
   }
   return EGPT_LAUNCH_STATUS();
@@ -564,6 +733,14 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
     // all 8 wavefronts on one 16-feature group: splitting K eight ways keeps the most
     // loads in flight (measured faster than 1, 2 or 4 wavefronts per group at every
     // Qwen3-1.7B shape, the 151936-row lm_head included)
+    // Wide outputs, K 1024-2048 in 512-byte chunks: the LDS-staged form (bit-identical to the walking one;
+    // against it, A/B on one box, cold, 3-16 rows: 151936 x 2048 70-80 -> 56-60 us, 12288 x 2048 8.9-10.1 ->
+    // 8.1-9.7, 70001 x 1024 20-22 -> 18-19, 20000 x 1536 11.7-12.9 -> 9.2-10.6; at K = 512 it was slower,
+    // 7.3-7.9 against 7.0-7.6 us at 32768 outputs).
+    if (K % kLdsChunk == 0 && K >= 2 * kLdsChunk && K <= 4 * kLdsChunk && N > kMfmaWalkMinN) {
+      if (N >= kMfmaWideN) return launch_mfma_lds<4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+      return launch_mfma_lds<1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+    }
     if (K <= 64 * kMfmaWaves * 4 && N > kMfmaWalkMinN) {
       if (N >= kMfmaWideN) return launch_mfma_walk<4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
       return launch_mfma_walk<1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);

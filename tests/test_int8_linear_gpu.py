@@ -225,13 +225,14 @@ def test_few_rows_equal_one_row_calls_bitwise(m, k, n):
 
 @pytest.mark.parametrize('m', [3, 4, 8, 16])
 @pytest.mark.parametrize('k,n', [(2048, 4096), (6144, 2048), (2048, 100), (12288, 48), (512, 32768), (1024, 70001),
-                                 (2048, 12288), (2048, 65600)])
+                                 (2048, 12288), (2048, 65600), (1536, 20000)])
 def test_small_batch_mfma_kernel_matches_oracle(m, k, n):
     """3-16 rows take the MFMA kernel (K a multiple of 64, aligned rows; 3-4 rows under 4096 features the
     few-rows kernel): against the oracle's decode rule, odd N, the longest K, 2048 feature groups (32768
     features), and an odd width past 65536 features, where each wavefront serves four groups of 16. Past 8192
-    features with K <= 2048 the blocks walk tiles (256 blocks): 12288 features at 3 tiles per block, 65600 (a
-    ragged last tile of four groups) at 4-5."""
+    features with K <= 2048 the blocks walk tiles; for K of 1024-2048 in 512-byte chunks the weights are staged
+    through LDS (12288 x 2048 and 20000 x 1536 with one group per tile, 65600 x 2048 and 70001 x 1024 with four,
+    a ragged last tile), at K = 512 they go to registers (32768 x 512)."""
     from efficientgpt_amd.int8_linear import int8_matmul
     x, q, s = make_case(m, k, n, seed=100 + m + k + n)
     xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
