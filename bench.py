@@ -31,10 +31,9 @@ Prints one JSON line:
                   replays timed, its GEMV launches timed on their own
   step            the whole step: weight + scale + KV bytes per token / ms per token
   copy_gbps       a device-to-device copy of 1 GiB, the measured bandwidth ceiling
-  cpu_baseline    the CPU oracle (oracle/qwen3.py, torch on the host) on a bounded
-                  sample of the same workload: prefill of the same prompt, then 32
-                  greedy tokens (--cpu-tokens; 256 is the whole decode), on the same
-                  weights; `kernels` holds the reference's CPU forms of the GEMV (every
+  cpu_baseline    the CPU oracle (oracle/qwen3.py, torch on the host) on the same
+                  workload: prefill of the same prompt, then all 256 greedy tokens
+                  (--cpu-tokens sets fewer), on the same weights; `kernels` holds the reference's CPU forms of the GEMV (every
                   shape, 1-8 rows) and the attention (every cache length) timed on the host
 """
 
@@ -64,8 +63,8 @@ def parse():
     ap.add_argument('--model', choices=('qwen3-1.7b', 'qwen3-8b'), default='qwen3-1.7b')
     ap.add_argument('--prompt', type=int, default=128)
     ap.add_argument('--seed', type=int, default=0)
-    ap.add_argument('--cpu-tokens', type=int, default=32,
-                    help='greedy tokens in the CPU baseline sample (0: skip; 256 is the full decode of the workload)')
+    ap.add_argument('--cpu-tokens', type=int, default=256,
+                    help='greedy tokens of the CPU baseline (0: skip; the default 256 is the whole decode of the workload)')
     ap.add_argument('--cpu-long-tokens', type=int, default=4,
                     help='CPU decode steps timed on the Qwen3-8B long-context weights (0: skip)')
     ap.add_argument('--no-long-context', action='store_true',
@@ -562,6 +561,28 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
         pos += 1
     t1 = time.perf_counter()
     decode_tps = (n_tokens - 1) / (t1 - t_first) if n_tokens > 1 else None
+    # Teacher-forced comparison (outside the CPU timing): the GPU step fed the oracle's own tokens, its pick at
+    # every step against the oracle's; a disagreement counts as a near-tie when the oracle's top-1 / top-2 margin
+    # is at most twice the GPU-oracle logit distance at that step (the reference's rule, widened as below).
+    with torch.inference_mode():
+        eng.reset()
+        got = eng.prefill(prompt)
+        tf_agree, tf_ties, tf_dist = 0, 0, 0.0
+        for i in range(n_tokens):
+            if i:
+                eng.token.fill_(toks[i - 1])
+                eng.replay()
+                got = eng.logits[0]
+            g = got.float().cpu()
+            dist = float((g - logits_at[i].float()).abs().max())
+            tf_dist = max(tf_dist, dist)
+            if int(torch.argmax(g)) == toks[i]:
+                tf_agree += 1
+            elif margins[i][0] <= 2 * dist:
+                tf_ties += 1
+    teacher_forced = (f'{tf_agree}/{n_tokens} steps pick the oracle\'s token; the other {n_tokens - tf_agree} are '
+                      f'near-ties: {tf_ties} of them (oracle margin <= twice the GPU-oracle logit distance, at most '
+                      f'{tf_dist:.3g} over the run)')
     gpu = list(gpu_tokens[:n_tokens])
     first = next((i for i, (a, b) in enumerate(zip(toks, gpu)) if a != b), None)
     agree = f'{n_tokens}/{n_tokens} identical'
@@ -592,7 +613,8 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
                        f'(n-1)/(total-TTFT)'),
             'ttft_s': round(t_first - t0, 3), 'total_s': round(t1 - t0, 3), 'tokens': n_tokens,
             'cpu': platform.processor() or platform.machine(),
-            'token_agreement_with_gpu': agree}
+            'token_agreement_with_gpu': agree, 'teacher_forced_agreement': teacher_forced,
+            'teacher_forced_agree': tf_agree, 'teacher_forced_near_ties': tf_ties}
 
 
 def dispatch_grid(inner=20, reps=20):
