@@ -163,13 +163,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attn_kernel(const Prefi
       }
     }
     // Online softmax of this lane's query over the tile's 64 slots (32 here, 32 in lane ^ 32).
+    // slots of the tile this lane's query sees: those at most lim past the tile's first
+    const int lim = (int)min((int64_t)kPfSlots, max((int64_t)-1, qpos - (int64_t)j * kPfSlots));
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t slot = (int64_t)j * kPfSlots + 32 * mt + 8 * (r / 4) + 4 * half + r % 4;
-        const float sv = slot <= qpos ? st[mt][r] * a.scale : -INFINITY;  // the fp32 logit (q . k) * scale
+        const int sl = 32 * mt + 8 * (r / 4) + 4 * half + r % 4;
+        const float sv = sl <= lim ? st[mt][r] * a.scale : -INFINITY;  // the fp32 logit (q . k) * scale
         st[mt][r] = sv;
         mx = fmaxf(mx, sv);
       }
