@@ -382,7 +382,7 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma_walk(
   }
 }
 
-// LDS-staged form of the walking GEMV, for K a multiple of 512 up to 2048. The
+// LDS-staged form of the walking GEMV, for K of 2, 3, 4, 6, 8 or 12 chunks of 512 bytes. The
 // MFMA operand layout puts 16 weight rows in every load instruction (64 bytes
 // of each): streamed that way an int8 matrix moves at 4.2 TB/s on the MI355X,
 // against 6.4 TB/s for loads that cover 1 KiB of consecutive bytes (a stream
@@ -580,6 +580,9 @@ int launch_mfma_lds(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw
     case 2: hipLaunchKernelGGL((gemv_i8_mfma_lds<2, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
     case 3: hipLaunchKernelGGL((gemv_i8_mfma_lds<3, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
     case 4: hipLaunchKernelGGL((gemv_i8_mfma_lds<4, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 6: hipLaunchKernelGGL((gemv_i8_mfma_lds<6, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 8: hipLaunchKernelGGL((gemv_i8_mfma_lds<8, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
+    case 12: hipLaunchKernelGGL((gemv_i8_mfma_lds<12, FG>), grid, block, 0, st, x, ldx, w, ldw, scale, y, ldy, M, N, K); break;
     default: return EGPT_ERR_UNSUPPORTED;
   }
   return EGPT_LAUNCH_STATUS();
@@ -733,13 +736,20 @@ extern "C" int egpt_int8_gemv(const void* x, int64_t ldx, const int8_t* w, int64
     // all 8 wavefronts on one 16-feature group: splitting K eight ways keeps the most
     // loads in flight (measured faster than 1, 2 or 4 wavefronts per group at every
     // Qwen3-1.7B shape, the 151936-row lm_head included)
-    // Wide outputs, K 1024-2048 in 512-byte chunks: the LDS-staged form (bit-identical to the walking one;
+    // Wide outputs, K of 1024-6144 in 512-byte chunks: the LDS-staged form (bit-identical to the walking one;
     // against it, A/B on one box, cold, 3-16 rows: 151936 x 2048 70-80 -> 56-60 us, 12288 x 2048 8.9-10.1 ->
     // 8.1-9.7, 70001 x 1024 20-22 -> 18-19, 20000 x 1536 11.7-12.9 -> 9.2-10.6; at K = 512 it was slower,
     // 7.3-7.9 against 7.0-7.6 us at 32768 outputs).
-    if (K % kLdsChunk == 0 && K >= 2 * kLdsChunk && K <= 4 * kLdsChunk && N > kMfmaWalkMinN) {
-      if (N >= kMfmaWideN) return launch_mfma_lds<4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
-      return launch_mfma_lds<1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+    // K of 3072-6144 (the Qwen3-8B rows) against gemv_i8_mfma: 151936 x 4096 152-163 -> 109-116 us, 24576 x 4096
+    // 26-38 -> 23-27. At 8192 outputs and fewer (one tile per block) it was slower: 4096 x 4096 8.1-10.1 against
+    // 7.3-8.7 us, 2048 x 6144 at 8-16 rows 11.8-13.8 against 9.3-11.2.
+    {
+      const int spw = K / kLdsChunk;
+      if (K % kLdsChunk == 0 && (spw == 2 || spw == 3 || spw == 4 || spw == 6 || spw == 8 || spw == 12) &&
+          N > kMfmaWalkMinN) {
+        if (N >= kMfmaWideN) return launch_mfma_lds<4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+        return launch_mfma_lds<1>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);
+      }
     }
     if (K <= 64 * kMfmaWaves * 4 && N > kMfmaWalkMinN) {
       if (N >= kMfmaWideN) return launch_mfma_walk<4>(xx, ldx, w, ldw, scale, yy, ldy, M, N, K, stream);

@@ -225,14 +225,14 @@ def test_few_rows_equal_one_row_calls_bitwise(m, k, n):
 
 @pytest.mark.parametrize('m', [3, 4, 8, 16])
 @pytest.mark.parametrize('k,n', [(2048, 4096), (6144, 2048), (2048, 100), (12288, 48), (512, 32768), (1024, 70001),
-                                 (2048, 12288), (2048, 65600), (1536, 20000)])
+                                 (2048, 12288), (2048, 65600), (1536, 20000), (4096, 12000), (6144, 9000)])
 def test_small_batch_mfma_kernel_matches_oracle(m, k, n):
     """3-16 rows take the MFMA kernel (K a multiple of 64, aligned rows; 3-4 rows under 4096 features the
     few-rows kernel): against the oracle's decode rule, odd N, the longest K, 2048 feature groups (32768
     features), and an odd width past 65536 features, where each wavefront serves four groups of 16. Past 8192
     features with K <= 2048 the blocks walk tiles; for K of 1024-2048 in 512-byte chunks the weights are staged
-    through LDS (12288 x 2048 and 20000 x 1536 with one group per tile, 65600 x 2048 and 70001 x 1024 with four,
-    a ragged last tile), at K = 512 they go to registers (32768 x 512)."""
+    through LDS (12288 x 2048, 20000 x 1536, 12000 x 4096 and 9000 x 6144 with one group per tile, 65600 x 2048
+    and 70001 x 1024 with four, a ragged last tile), at K = 512 they go to registers (32768 x 512)."""
     from efficientgpt_amd.int8_linear import int8_matmul
     x, q, s = make_case(m, k, n, seed=100 + m + k + n)
     xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
@@ -240,6 +240,17 @@ def test_small_batch_mfma_kernel_matches_oracle(m, k, n):
     check_against_oracle(y.cpu(), x, q, s)
     again = int8_matmul(xd, qd, sd)
     assert torch.equal(y, again)  # fixed reduction order: reproducible
+
+
+def test_small_batch_lds_kernel_four_groups_long_rows():
+    """8 rows over 65600 x 3072: the LDS-staged MFMA GEMV with four feature groups per tile and six 512-byte
+    chunks per row, a ragged last tile; against the oracle, reproducible."""
+    from efficientgpt_amd.int8_linear import int8_matmul
+    x, q, s = make_case(8, 3072, 65600, seed=77)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    y = int8_matmul(xd, qd, sd)
+    check_against_oracle(y.cpu(), x, q, s)
+    assert torch.equal(y, int8_matmul(xd, qd, sd))
 
 
 PREFILL_SHAPES = [(17, 64, 64), (33, 2048, 4096), (128, 2048, 4096), (100, 2048, 6144), (300, 6144, 2048),
