@@ -8,11 +8,13 @@
 // static cache, HF models/qwen3/modeling_qwen3.py), for which the decode kernels
 // would rescan the prefix once per query row. bf16 q, k, v and output; the logits
 // (q . k) * scale and the online softmax in fp32; the probabilities enter the
-// p . v products as bf16, as in SDPA's bf16 flash path.
+// p . v products as bf16, as in SDPA's bf16 flash path; the softmax runs in the
+// units of the raw scores, p = 2^((q.k - max) * scale * log2 e), the flash form's
+// folded scale.
 //
-// A block is 4 wavefronts over one kv head; each wavefront owns 32 consecutive
+// A block is 8 wavefronts over one kv head; each wavefront owns 32 consecutive
 // query rows of one query head, so a block covers min(group, 4) query heads and
-// 32 * 4 / min(group, 4) positions, and every head of the block shares the K/V
+// 32 * 8 / min(group, 4) positions, and every head of the block shares the K/V
 // tiles it stages. K/V advance 64 slots at a time through two LDS buffers (the
 // global loads of tile j + 1 are issued before tile j is multiplied).
 //
@@ -41,7 +43,9 @@ typedef float f32x16_pf __attribute__((ext_vector_type(16)));
 
 constexpr int kPfD = 128;              // head dim
 constexpr int kPfSlots = 64;           // K/V slots per tile
-constexpr int kPfThreads = 256;        // 4 wavefronts
+constexpr int kPfWaves = 8;
+constexpr int kPfThreads = kPfWaves * 64;
+constexpr int kPfStage = kPfThreads / 2;  // threads staging K (and as many staging V)
 constexpr int kPfKRow = kPfD + 8;      // bf16 per K row in LDS (16 bytes of padding)
 constexpr int kPfVRow = kPfSlots + 8;  // bf16 per V^T row in LDS
 constexpr float kPfLog2e = 1.4426950408889634f;
@@ -64,7 +68,7 @@ struct PrefillArgs {
 // Position of slot s (0..15 of a 16-slot step) in the staged V^T row: bits 2 and 3 swapped.
 __device__ __forceinline__ int vperm(int s) { return (s & 3) | ((s >> 2 & 1) << 3) | ((s >> 3 & 1) << 2); }
 
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_attn_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const PrefillArgs a) {
   __shared__ __align__(16) uint16_t Ks[2][kPfSlots * kPfKRow];
   __shared__ __align__(16) uint16_t Vs[2][kPfD * kPfVRow];
 
@@ -98,42 +102,46 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attn_kernel(const Prefi
     for (int kk = 0; kk < kPfD / 16; ++kk) qf[kk] = ld16(qrow + 16 * kk);
   }
 
-  // Staging of one K/V tile: 64 slots x 16 chunks of 8 dims each for K and V. A
-  // thread takes K chunks (slot c / 16, chunk c % 16) for c = tid + 256 i, and V
-  // chunk `vc` of the four consecutive slots 4 vg .. 4 vg + 3, whose staged
-  // positions are consecutive too (vperm keeps bits 0 and 1), so each of its 8
-  // dims is one 8-byte LDS store.
+  // Staging of one K/V tile: 64 slots x 16 chunks of 8 dims each for K and V. The
+  // first 4 wavefronts stage V, the other 4 K, so every thread keeps four 16-byte
+  // loads in flight. A K thread t takes chunks (slot c / 16, chunk c % 16) for c =
+  // t + 256 i; a V thread t takes chunk vc = t % 16 of the four consecutive slots
+  // 4 vg .. 4 vg + 3 (vg = t / 16), whose staged positions are consecutive too
+  // (vperm keeps bits 0 and 1), so each of its 8 dims is one 8-byte LDS store.
   const uint16_t* kb = a.k + (int64_t)hk * a.c_sh;
   const uint16_t* vb = a.v + (int64_t)hk * a.c_sh;
-  const int vg = tid / 16, vc = tid % 16;
-  u32x4 kr[4], vr[4];
+  const int stid = tid % kPfStage;
+  const bool do_k = tid >= kPfStage;  // wave-uniform
+  const int vg = stid / 16, vc = stid % 16;
+  u32x4 sr[4];
   auto gload = [&](int j) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = tid + kPfThreads * i;
-      const int64_t s = min((int64_t)j * kPfSlots + c / 16, last);
-      kr[i] = ld16(kb + s * a.c_sn + (c % 16) * 8);
-      const int64_t sv = min((int64_t)j * kPfSlots + 4 * vg + i, last);
-      vr[i] = ld16(vb + sv * a.c_sn + vc * 8);
+      const int c = stid + kPfStage * i;
+      const int64_t s = min((int64_t)j * kPfSlots + (do_k ? c / 16 : 4 * vg + i), last);
+      sr[i] = ld16((do_k ? kb : vb) + s * a.c_sn + (do_k ? c % 16 : vc) * 8);
     }
   };
   auto lstore = [&](int buf) {
+    if (do_k) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + kPfThreads * i;
-      *(u32x4*)&Ks[buf][(c / 16) * kPfKRow + (c % 16) * 8] = kr[i];
-    }
-    // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions
-    const int p0 = (4 * vg) & ~15;
-    const int p = p0 + vperm((4 * vg) & 15);
+      for (int i = 0; i < 4; ++i) {
+        const int c = stid + kPfStage * i;
+        *(u32x4*)&Ks[buf][(c / 16) * kPfKRow + (c % 16) * 8] = sr[i];
+      }
+    } else {
+      // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions
+      const int p0 = (4 * vg) & ~15;
+      const int p = p0 + vperm((4 * vg) & 15);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int sh = 16 * (e & 1);
-      const uint32_t w0 = ((e < 2 ? vr[0].x : e < 4 ? vr[0].y : e < 6 ? vr[0].z : vr[0].w) >> sh) & 0xffffu;
-      const uint32_t w1 = ((e < 2 ? vr[1].x : e < 4 ? vr[1].y : e < 6 ? vr[1].z : vr[1].w) >> sh) & 0xffffu;
-      const uint32_t w2 = ((e < 2 ? vr[2].x : e < 4 ? vr[2].y : e < 6 ? vr[2].z : vr[2].w) >> sh) & 0xffffu;
-      const uint32_t w3 = ((e < 2 ? vr[3].x : e < 4 ? vr[3].y : e < 6 ? vr[3].z : vr[3].w) >> sh) & 0xffffu;
-      *(uint2*)&Vs[buf][(vc * 8 + e) * kPfVRow + p] = make_uint2(w0 | (w1 << 16), w2 | (w3 << 16));
+      for (int e = 0; e < 8; ++e) {
+        const int sh = 16 * (e & 1);
+        const uint32_t w0 = ((e < 2 ? sr[0].x : e < 4 ? sr[0].y : e < 6 ? sr[0].z : sr[0].w) >> sh) & 0xffffu;
+        const uint32_t w1 = ((e < 2 ? sr[1].x : e < 4 ? sr[1].y : e < 6 ? sr[1].z : sr[1].w) >> sh) & 0xffffu;
+        const uint32_t w2 = ((e < 2 ? sr[2].x : e < 4 ? sr[2].y : e < 6 ? sr[2].z : sr[2].w) >> sh) & 0xffffu;
+        const uint32_t w3 = ((e < 2 ? sr[3].x : e < 4 ? sr[3].y : e < 6 ? sr[3].z : sr[3].w) >> sh) & 0xffffu;
+        *(uint2*)&Vs[buf][(vc * 8 + e) * kPfVRow + p] = make_uint2(w0 | (w1 << 16), w2 | (w3 << 16));
+      }
     }
   };
 
@@ -162,30 +170,40 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_attn_kernel(const Prefi
                                                          __builtin_bit_cast(bf16x8_pf, qf[kk]), st[mt], 0, 0, 0);
       }
     }
-    // Online softmax of this lane's query over the tile's 64 slots (32 here, 32 in lane ^ 32).
-    // slots of the tile this lane's query sees: those at most lim past the tile's first
-    const int lim = (int)min((int64_t)kPfSlots, max((int64_t)-1, qpos - (int64_t)j * kPfSlots));
+    // Online softmax of this lane's query over the tile's 64 slots (32 here, 32 in
+    // lane ^ 32), in the units of the raw scores q . k: the scale is positive, so
+    // the maximum commutes with it, and p = 2^((s - m) * scale * log2 e) takes one
+    // FMA and one exp2 per slot. Tiles wholly at or before the wavefront's first
+    // position need no causal mask (wave-uniform).
+    if ((int64_t)j * kPfSlots + kPfSlots - 1 > (int64_t)a.pos0 + tw) {
+      // slots of the tile this lane's query sees: those at most lim past the tile's first
+      const int lim = (int)min((int64_t)kPfSlots, max((int64_t)-1, qpos - (int64_t)j * kPfSlots));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int sl = 32 * mt + 8 * (r / 4) + 4 * half + r % 4;
+          st[mt][r] = sl <= lim ? st[mt][r] : -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int sl = 32 * mt + 8 * (r / 4) + 4 * half + r % 4;
-        const float sv = sl <= lim ? st[mt][r] * a.scale : -INFINITY;  // the fp32 logit (q . k) * scale
-        st[mt][r] = sv;
-        mx = fmaxf(mx, sv);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
     LanePair pr = pair32(mx);
     mx = fmaxf(pr.lo, pr.hi);
     const float mn = fmaxf(m, mx);
     const float mref = mn == -INFINITY ? 0.f : mn;
-    const float alpha = __builtin_amdgcn_exp2f((m - mref) * kPfLog2e);
+    const float c = a.scale * kPfLog2e;
+    const float alpha = __builtin_amdgcn_exp2f((m - mref) * c);
+    const float off = -mref * c;
     float ps = 0.f;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f((st[mt][r] - mref) * kPfLog2e);  // 0 for masked slots
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[mt][r], c, off));  // 0 for masked slots
         st[mt][r] = p;
         ps += p;
       }
@@ -245,7 +263,8 @@ using namespace egpt;
 extern "C" int egpt_prefill_attn(const void* q, int64_t q_ld, const void* k, const void* v, int64_t c_sh,
                                  int64_t c_sn, void* out, int64_t o_ld, int rows, int Hq, int Hkv, int D, int cap,
                                  int pos0, float scale, hipStream_t stream) {
-  if (!q || !k || !v || !out || rows < 0 || Hq < 1 || Hkv < 1 || Hq % Hkv || cap < 1 || pos0 < 0) return EGPT_ERR_INVALID;
+  if (!q || !k || !v || !out || rows < 0 || Hq < 1 || Hkv < 1 || Hq % Hkv || cap < 1 || pos0 < 0 || !(scale > 0.f))
+    return EGPT_ERR_INVALID;
   if (rows == 0) return EGPT_OK;
   if ((int64_t)pos0 + rows > cap) return EGPT_ERR_INVALID;
   if (D != kPfD) return EGPT_ERR_UNSUPPORTED;
@@ -268,7 +287,7 @@ extern "C" int egpt_prefill_attn(const void* q, int64_t q_ld, const void* k, con
   a.group = group;
   a.pos0 = pos0;
   a.hb = group < 4 ? group : 4;
-  a.bt = 32 * 4 / a.hb;
+  a.bt = 32 * kPfWaves / a.hb;
   a.ntiles = (rows + a.bt - 1) / a.bt;
   a.scale = scale;
   const dim3 grid((unsigned)(Hkv * (group / a.hb)), (unsigned)a.ntiles);

@@ -182,8 +182,8 @@ int egpt_qk_norm_rope(const void *qkv, int64_t ld_qkv, const int64_t *positions,
  * rotated queries of egpt_qk_norm_rope), caches [Hkv, cap, D] (strides cache_head_stride,
  * cache_slot_stride) already holding slots 0 .. pos0 + rows - 1, bf16 out [rows, Hq*D]
  * (row stride o_ld). fp32 logits and softmax; the probabilities multiply v as bf16.
- * D 128, Hq / Hkv in {1, 2, 4, 8} (else EGPT_ERR_UNSUPPORTED: the caller keeps its
- * library attention). */
+ * scale > 0 (else EGPT_ERR_INVALID). D 128, Hq / Hkv in {1, 2, 4, 8} (else
+ * EGPT_ERR_UNSUPPORTED: the caller keeps its library attention). */
 int egpt_prefill_attn(const void *q, int64_t q_ld, const void *k_cache, const void *v_cache,
                       int64_t cache_head_stride, int64_t cache_slot_stride, void *out, int64_t o_ld, int rows,
                       int Hq, int Hkv, int D, int cap, int pos0, float scale, hipStream_t stream);

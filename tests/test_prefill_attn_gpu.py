@@ -106,4 +106,6 @@ def test_prefill_attention_refuses_what_it_does_not_take():
     assert call(hq=24, hkv=8) == _lib.EGPT_ERR_UNSUPPORTED  # 3 query heads per kv head
     assert call(pos0=29) < 0 and call(pos0=29) != _lib.EGPT_ERR_UNSUPPORTED  # pos0 + rows past the cache
     assert call(rows=0) == _lib.EGPT_OK
+    assert lib.egpt_prefill_attn(q.data_ptr(), q.stride(0), kv.data_ptr(), kv.data_ptr(), kv.stride(0), kv.stride(1),
+                                 out.data_ptr(), out.stride(0), 4, 16, 8, D, 32, 0, -0.1, _lib.stream_ptr()) < 0
     torch.cuda.synchronize()
