@@ -66,8 +66,9 @@ __device__ __forceinline__ bf16x8 int8x8_to_bf16(const uint32_t w0, const uint32
     const float f1 = (float)(int)(int8_t)((w[i] >> 8) & 0xffu);
     const float f2 = (float)(int)(int8_t)((w[i] >> 16) & 0xffu);
     const float f3 = (float)(int)(int8_t)(w[i] >> 24);
-    o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-    o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+    // the upper halves of two floats in one v_perm_b32 (bytes 2, 3 of f0, then of f1)
+    o[2 * i] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    o[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
   }
   return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
@@ -288,18 +289,24 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
   }
 }
 
-// Split-K reduce: y[m, n] = bf16(bf16(sum_s part[s][m][n]) * scale[n]), splits added in order.
+// Split-K reduce: y[m, n] = bf16(bf16(sum_s part[s][m][n]) * scale[n]), splits added in order. The split
+// count is a template argument so that every slice's load is issued before the first addition.
 constexpr int kReduceThreads = 256;
 
+template <int S>
 __global__ __launch_bounds__(kReduceThreads) void int8_gemm_reduce_kernel(const float* __restrict__ part,
                                                                           const float* __restrict__ scale,
                                                                           uint16_t* __restrict__ y, int64_t ldy, int M,
-                                                                          int N, int splits) {
+                                                                          int N) {
   const int64_t mn = (int64_t)M * N;
   for (int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x; i < mn;
        i += (int64_t)gridDim.x * kReduceThreads) {
-    float acc = part[i];
-    for (int sp = 1; sp < splits; ++sp) acc += part[sp * mn + i];
+    float v[S];
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) v[sp] = part[sp * mn + i];
+    float acc = v[0];
+#pragma unroll
+    for (int sp = 1; sp < S; ++sp) acc += v[sp];
     const int64_t m = i / N, n = i - m * N;
     y[m * ldy + n] = f32_to_bf16(bf16_to_f32(f32_to_bf16(acc)) * scale[n]);
   }
@@ -308,6 +315,21 @@ __global__ __launch_bounds__(kReduceThreads) void int8_gemm_reduce_kernel(const 
 template <int BM, int BN>
 unsigned gemm_blocks(const GemmArgs& a) {
   return (unsigned)(((int64_t)a.N + BN - 1) / BN) * (unsigned)(((int64_t)a.M + BM - 1) / BM);
+}
+
+constexpr int kMaxSplits = 16;
+
+// The reduce for a.splits (2 ... S) slices; false for a count outside that range.
+template <int S>
+bool launch_reduce(const GemmArgs& a, unsigned blocks, hipStream_t st) {
+  if constexpr (S < 2) {
+    return false;
+  } else {
+    if (a.splits != S) return launch_reduce<S - 1>(a, blocks, st);
+    hipLaunchKernelGGL(int8_gemm_reduce_kernel<S>, dim3(blocks), dim3(kReduceThreads), 0, st, a.part, a.scale, a.y,
+                       a.ldy, a.M, a.N);
+    return true;
+  }
 }
 
 template <int BM, int BN, int WN = 2, int NW = 4>
@@ -322,8 +344,7 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
       if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
       const int64_t mn = (int64_t)a.M * a.N;
       const unsigned blocks = (unsigned)std::min<int64_t>((mn + kReduceThreads - 1) / kReduceThreads, 4096);
-      hipLaunchKernelGGL(int8_gemm_reduce_kernel, dim3(blocks), dim3(kReduceThreads), 0, st, a.part, a.scale, a.y,
-                         a.ldy, a.M, a.N, a.splits);
+      if (!launch_reduce<kMaxSplits>(a, blocks, st)) return EGPT_ERR_INVALID;
       return EGPT_LAUNCH_STATUS();
     }
   }
@@ -336,7 +357,6 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
 // of kBKSplit and at least 256 wide. 1 when the tiles already fill the chip, or K
 // is short or not a multiple of kBKSplit.
 constexpr int kMinSliceSteps = 4;
-constexpr int kMaxSplits = 16;
 constexpr int kSplitTargetBlocks = 256;
 
 void gemm_split(int64_t M, int64_t N, int64_t K, int& splits, int& kchunk) {
