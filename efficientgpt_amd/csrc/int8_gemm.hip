@@ -202,21 +202,51 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
 
   // The MFMAs of one K step from LDS buffer `buf`, 16 K columns at a time.
   auto mma_step = [&](int buf) {
+    if constexpr (TM * TN <= 2) {
+      // Small tiles run one wavefront per SIMD with a short MFMA chain per K sub-step, so
+      // nothing would cover an LDS read issued just before its MFMA: read every fragment
+      // of the step first, then convert and multiply.
+      bf16x8 af[BK / 16][TM];
+      uint32_t bw[BK / 16][TN][2];
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 af[TM], bfr[TN];
+      for (int ks = 0; ks < BK / 16; ++ks) {
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm) af[tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
+        for (int tm = 0; tm < TM; ++tm) af[ks][tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
-        bfr[tn] = int8x8_to_bf16(p[0], p[1]);
+        for (int tn = 0; tn < TN; ++tn) {
+          const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
+          bw[ks][tn][0] = p[0];
+          bw[ks][tn][1] = p[1];
+        }
       }
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8 bfr[TN];
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn)
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bfr[tn], acc[tm][tn], 0, 0, 0);
+        for (int tn = 0; tn < TN; ++tn) bfr[tn] = int8x8_to_bf16(bw[ks][tn][0], bw[ks][tn][1]);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][tm], bfr[tn], acc[tm][tn], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8 af[TM], bfr[TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) af[tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
+          bfr[tn] = int8x8_to_bf16(p[0], p[1]);
+        }
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bfr[tn], acc[tm][tn], 0, 0, 0);
+      }
     }
   };
 
