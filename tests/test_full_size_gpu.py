@@ -21,7 +21,10 @@ whole model. Parity is: every step's GPU logits within twice that noise of the
 oracle's, and greedy agreement with the oracle no worse than the two reference forms'
 agreement with each other, less 3% of the steps. A disagreement is then a near-tie by
 construction: the oracle's margin between its pick and the GPU's is at most twice
-their logit distance. The reference's decoder test compares tokens with generate's
+their logit distance. The 99% bar applies where rounding cannot decide a pick: on
+every step whose oracle top-1 / top-2 margin exceeds twice the two reference forms'
+distance at that step (at least a quarter of the steps), the GPU must pick the
+oracle's token at least 99% of the time. The reference's decoder test compares tokens with generate's
 (research/realmodel/test_fast_decode.py:26-40) on a tiny model, where rounding never
 decides a pick; the tiny-model tests here keep its exact-match bar.
 
@@ -115,6 +118,19 @@ def test_qwen3_1p7b_full_model_256_greedy_tokens_match_oracle():
         p = int(picks[i])
         if p != got[i]:
             assert float(want[i, p] - want[i, got[i]]) <= 2 * float(dev[i]) + 1e-6, i
+    # The 99% bar on the steps whose pick is decided by the model rather than by rounding: the oracle's top-1 /
+    # top-2 margin exceeds twice the distance between the reference's two GEMV forms at that step, so neither of
+    # them can flip it. The GPU must pick the oracle's token on at least 99% of those steps, and they must be a
+    # sizeable share of the run (a bar over a handful of steps would pin nothing).
+    top2 = want.topk(2, dim=1).values
+    margin = top2[:, 0] - top2[:, 1]
+    decided = margin > 2 * (other - want).abs().amax(1)
+    n_decided = int(decided.sum())
+    agree_decided = int(((picks == torch.tensor(got)) & decided).sum())
+    print(f'1.7B: {n_decided}/{new} steps decided beyond the reference forms\' noise, GPU agrees on '
+          f'{agree_decided}', flush=True)
+    assert n_decided >= new // 4, n_decided
+    assert agree_decided >= 0.99 * n_decided, (agree_decided, n_decided)
 
 
 def _qwen3_8b_long_prompt():
