@@ -64,7 +64,7 @@ def save_engine(path, engine):
 def load_int8(path, device='cpu'):
     """(Qwen3Config, packed layout, inv_freq or None) from `path`; raises ValueError on a foreign file."""
     from safetensors import safe_open
-    from .qwen3 import Qwen3Config
+    from .qwen3 import Qwen3Config, check_packed
     with safe_open(path, framework='pt', device=str(device)) as f:
         meta = f.metadata() or {}
         if meta.get('format') != FORMAT:
@@ -84,31 +84,5 @@ def load_int8(path, device='cpu'):
         packed = {'layers': layers, 'embed': get('embed'), 'norm_w': get('final_norm'),
                   'head_q': get('lm_head.qweight'), 'head_s': get('lm_head.scale')}
         inv_freq = get('rope.inv_freq') if 'rope.inv_freq' in names else None
-    _check(cfg, packed)
+    check_packed(cfg, packed)  # a truncated or mismatched file fails here
     return cfg, packed, inv_freq
-
-
-def _expect(what, t, dtype, shape):
-    if t.dtype != dtype or tuple(t.shape) != tuple(shape):
-        raise ValueError(f'{what}: {t.dtype} {tuple(t.shape)}, expected {dtype} {tuple(shape)}')
-
-
-def _check(cfg, packed):
-    """Every stored tensor's dtype and shape against the config: a truncated or mismatched file fails here, not in a
-    kernel that would read past the end of a short tensor."""
-    d, hq, hkv = cfg.head_dim, cfg.heads, cfg.kv_heads
-    want = {'qkv_q': ((hq + 2 * hkv) * d, cfg.hidden), 'o_q': (cfg.hidden, hq * d), 'gu_q': (2 * cfg.inter, cfg.hidden),
-            'down_q': (cfg.hidden, cfg.inter)}
-    norms = {'in_w': cfg.hidden, 'post_w': cfg.hidden, 'qn_w': d, 'kn_w': d}
-    if len(packed['layers']) != cfg.layers:
-        raise ValueError(f'{len(packed["layers"])} layers stored, the config has {cfg.layers}')
-    for i, L in enumerate(packed['layers']):
-        for key, shape in want.items():
-            _expect(f'layer {i} {key}', L[key], torch.int8, shape)
-            _expect(f'layer {i} {key[:-1]}s', L[key[:-1] + 's'], torch.float32, (shape[0],))
-        for key, n in norms.items():
-            _expect(f'layer {i} {key}', L[key], torch.bfloat16, (n,))
-    _expect('embed', packed['embed'], torch.bfloat16, (cfg.vocab, cfg.hidden))
-    _expect('final_norm', packed['norm_w'], torch.bfloat16, (cfg.hidden,))
-    _expect('lm_head qweight', packed['head_q'], torch.int8, (cfg.vocab, cfg.hidden))
-    _expect('lm_head scale', packed['head_s'], torch.float32, (cfg.vocab,))

@@ -144,6 +144,33 @@ def pack_qwen3(cfg, weights):
             'head_q': hq, 'head_s': hs.float()}
 
 
+def _expect(what, t, dtype, shape):
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape):
+        raise ValueError(f'{what}: {t.dtype} {tuple(t.shape)}, expected {dtype} {tuple(shape)}')
+
+
+def check_packed(cfg, packed):
+    """Every tensor of the packed layout (pack_qwen3's result, or a checkpoint's) against the config, dtype and
+    shape: weights that do not match fail here (ValueError), not in a kernel that would read past the end of a
+    short tensor."""
+    d, hq, hkv = cfg.head_dim, cfg.heads, cfg.kv_heads
+    want = {'qkv_q': ((hq + 2 * hkv) * d, cfg.hidden), 'o_q': (cfg.hidden, hq * d), 'gu_q': (2 * cfg.inter, cfg.hidden),
+            'down_q': (cfg.hidden, cfg.inter)}
+    norms = {'in_w': cfg.hidden, 'post_w': cfg.hidden, 'qn_w': d, 'kn_w': d}
+    if len(packed['layers']) != cfg.layers:
+        raise ValueError(f'{len(packed["layers"])} layers given, the config has {cfg.layers}')
+    for i, L in enumerate(packed['layers']):
+        for key, shape in want.items():
+            _expect(f'layer {i} {key}', L[key], torch.int8, shape)
+            _expect(f'layer {i} {key[:-1]}s', L[key[:-1] + 's'], torch.float32, (shape[0],))
+        for key, n in norms.items():
+            _expect(f'layer {i} {key}', L[key], torch.bfloat16, (n,))
+    _expect('embed', packed['embed'], torch.bfloat16, (cfg.vocab, cfg.hidden))
+    _expect('final_norm', packed['norm_w'], torch.bfloat16, (cfg.hidden,))
+    _expect('lm_head qweight', packed['head_q'], torch.int8, (cfg.vocab, cfg.hidden))
+    _expect('lm_head scale', packed['head_s'], torch.float32, (cfg.vocab,))
+
+
 class Qwen3Int8Engine:
     """Static-cache batch-1 Qwen3 decoder with int8 linears; one graph replay per token.
 
@@ -164,6 +191,7 @@ class Qwen3Int8Engine:
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
 
         pk = weights if packed else pack_qwen3(c, weights)
+        check_packed(c, pk)
         self.layers = [{k: put(v) for k, v in L.items()} for L in pk['layers']]
         self.embed = put(pk['embed'], bf)
         self.norm_w = put(pk['norm_w'], bf)

@@ -77,3 +77,22 @@ def test_every_stored_tensor_is_checked(tmp_path, key, cut):
     checkpoint.save_int8(bad, CFG, pk)
     with pytest.raises(ValueError, match=match):
         checkpoint.load_int8(bad)
+
+
+@pytest.mark.parametrize('packed', [True, False])
+def test_engine_refuses_weights_that_do_not_match_the_config(packed):
+    """The engine checks the packed layout itself, whatever it was built from (packed tensors, or transformers-named
+    weights through pack_qwen3): a short q_proj or o_proj raises before any tensor reaches the device."""
+    from efficientgpt_amd.qwen3 import Qwen3Int8Engine
+    w = quantize_weights(random_weights(TINY, seed=5, std=0.2), TINY)
+    if packed:
+        pk = pack_qwen3(CFG, w)
+        pk['layers'][0]['o_q'] = pk['layers'][0]['o_q'][:, :-16].contiguous()
+        arg, match = pk, 'layer 0 o_q'
+    else:
+        name = 'model.layers.1.self_attn.q_proj'
+        w[name + '.qweight'] = w[name + '.qweight'][:-8].contiguous()
+        w[name + '.scale'] = w[name + '.scale'][:-8].contiguous()
+        arg, match = w, 'layer 1 qkv_q'
+    with pytest.raises(ValueError, match=match):
+        Qwen3Int8Engine(CFG, arg, 16, device='cpu', packed=packed)
