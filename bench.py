@@ -723,6 +723,10 @@ def main():
             g0 = extra['gemv_1x2048_6144']
             g0['frac_beyond_floor'] = round(g0['bytes_per_call'] / max(g0['us_per_call'] - floor, 1e-3) / 1e3
                                             / HBM_PEAK_GBPS, 4)
+            # the dominant kernel family likewise: the step's GEMV launches less one floor each
+            roof['frac_beyond_floor'] = round(
+                roof['bytes_per_step'] / max(roof['gemv_ms_per_step'] * 1e3 - roof['launches'] * floor, 1e-3)
+                / 1e3 / HBM_PEAK_GBPS, 4)
             for L, r in list(extra['attention_by_length'].items()) + [('32768', extra['attention'])]:
                 launches = 1 if r['nsplit'] == 1 else 2  # the split kernel, then the combine
                 r['frac_beyond_floor'] = round((4096 * int(L) + 8192) / max(r['us_per_call'] - launches * floor, 1e-3)
