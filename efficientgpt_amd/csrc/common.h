@@ -204,6 +204,14 @@ constexpr int kGemvFewRowsWideN = 4096;
 int gemv_few_rows(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y, int64_t ldy,
                   int M, int N, int K, hipStream_t st);
 
+// The split-K prefill GEMM's partials [splits][M][N] (fp32, in the workspace) added in split order and rounded
+// as int8_gemm_reduce_kernel does, o = bf16(bf16(sum) * scale[n]), then the residual update and RMSNorm of each
+// row as add_rmsnorm_kernel does: resid = bf16(resid + o) (written back), y = RMSNorm(resid) * norm_w. One block
+// per row; the same per-thread element order and block sum as add_rmsnorm_kernel, so the result is bit-identical
+// to the reduce launch followed by egpt_add_rmsnorm. Defined with the norm kernels (qwen3_step.hip).
+int launch_reduce_add_rmsnorm(const float* part, int splits, const float* scale, void* resid, int64_t ld_resid,
+                              const void* norm_w, void* y, int64_t ldy, int M, int N, float eps, hipStream_t st);
+
 }  // namespace egpt
 
 // Map a HIP launch result to the library's status convention.

@@ -362,16 +362,24 @@ bool launch_reduce(const GemmArgs& a, unsigned blocks, hipStream_t st) {
   }
 }
 
+// The split slices' fp32 tiles into a.part (64 x 64 tiles, a.splits > 1); no reduce.
+int launch_split_partials(GemmArgs a, hipStream_t st) {
+  a.tiles_m = (int)(((int64_t)a.M + 63) / 64);
+  a.tiles_n = (int)(((int64_t)a.N + 63) / 64);
+  const unsigned tiles = (unsigned)a.tiles_m * (unsigned)a.tiles_n;
+  hipLaunchKernelGGL((int8_gemm_kernel<64, 64, kBKSplit, true, 2, 4>), dim3(tiles * (unsigned)a.splits),
+                     dim3(4 * kWave), 0, st, a);
+  return EGPT_LAUNCH_STATUS();
+}
+
 template <int BM, int BN, int WN = 2, int NW = 4>
 int launch_gemm(GemmArgs a, hipStream_t st) {
   a.tiles_m = (int)(((int64_t)a.M + BM - 1) / BM);
   a.tiles_n = (int)(((int64_t)a.N + BN - 1) / BN);
   const unsigned tiles = (unsigned)a.tiles_m * (unsigned)a.tiles_n;
-  if constexpr (BM == 64 && BN == 64) {  // split-K runs 64 x 64 tiles
+  if constexpr (BM == 64 && BN == 64 && WN == 2 && NW == 4) {  // split-K runs 64 x 64 tiles
     if (a.splits > 1) {
-      hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBKSplit, true, WN, NW>), dim3(tiles * (unsigned)a.splits),
-                         dim3(NW * kWave), 0, st, a);
-      if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
+      if (launch_split_partials(a, st) != EGPT_OK) return EGPT_ERR_LAUNCH;
       const int64_t mn = (int64_t)a.M * a.N;
       const unsigned blocks = (unsigned)std::min<int64_t>((mn + kReduceThreads - 1) / kReduceThreads, 4096);
       if (!launch_reduce<kMaxSplits>(a, blocks, st)) return EGPT_ERR_INVALID;
@@ -445,6 +453,30 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
   if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128, kWN128, kNW128>(a, stream);
   if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
   return launch_gemm<64, 64>(a, stream);
+}
+
+extern "C" int egpt_int8_gemm_add_rmsnorm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw,
+                                          const float* scale, void* resid, int64_t ld_resid, const void* norm_w,
+                                          void* y, int64_t ldy, int M, int N, int K, float eps, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+  if (!x || !w || !scale || !resid || !norm_w || !y || M < 0 || N < 0 || K < 0) return EGPT_ERR_INVALID;
+  if (ldx < K || ldw < K || ld_resid < N || ldy < N) return EGPT_ERR_INVALID;
+  if (M == 0 || N == 0) return EGPT_OK;
+  if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
+    return EGPT_ERR_UNSUPPORTED;
+  if ((int64_t)M * ldx * 2 >= ((int64_t)1 << 31) || (int64_t)N * ldw >= ((int64_t)1 << 31)) return EGPT_ERR_UNSUPPORTED;
+  if ((size_t)N * sizeof(float) > 64 * 1024) return EGPT_ERR_UNSUPPORTED;  // the row kernel stages a row in LDS
+  int splits, kchunk;
+  gemm_split(M, N, K, splits, kchunk);
+  if (splits < 2) return EGPT_ERR_UNSUPPORTED;  // nothing to fold: egpt_int8_gemm_ws, then egpt_add_rmsnorm
+  if (!workspace || workspace_bytes < (size_t)splits * (size_t)M * (size_t)N * sizeof(float) ||
+      (uintptr_t)workspace % 16)
+    return EGPT_ERR_WORKSPACE;
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, nullptr, N, M, N, K, 0, 0, splits, kchunk, (float*)workspace};
+  const int st = launch_split_partials(a, stream);
+  if (st != EGPT_OK) return st;
+  return launch_reduce_add_rmsnorm((const float*)workspace, splits, scale, resid, ld_resid, norm_w, y, ldy, M, N,
+                                   eps, stream);
 }
 
 extern "C" int egpt_int8_gemm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y,

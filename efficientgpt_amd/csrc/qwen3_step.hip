@@ -213,7 +213,71 @@ __global__ __launch_bounds__(kArgThreads) void argmax_final_kernel(const float* 
 
 constexpr int kArgParts = 256;
 
+// launch_reduce_add_rmsnorm's kernel: S split partials per element, every load of an element issued before its
+// first addition (the reduce kernel's order: v0 + v1 + ... + v(S-1)).
+template <int S>
+__global__ __launch_bounds__(kNormThreads) void reduce_add_rmsnorm_kernel(const float* __restrict__ part,
+                                                                         const float* __restrict__ scale,
+                                                                         uint16_t* __restrict__ x, int64_t ldx,
+                                                                         const uint16_t* __restrict__ w,
+                                                                         uint16_t* __restrict__ y, int64_t ldy, int M,
+                                                                         int n, float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  extern __shared__ float rowbuf[];  // n floats: the updated residual row
+  const int64_t row = blockIdx.x;
+  const int64_t mn = (int64_t)M * n;
+  const float* pr = part + row * n;
+  uint16_t* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += kNormThreads) {
+    float v[S];
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) v[sp] = pr[sp * mn + i];
+    float acc = v[0];
+#pragma unroll
+    for (int sp = 1; sp < S; ++sp) acc += v[sp];
+    const float o = bf16r(bf16r(acc) * scale[i]);  // the GEMM's output element, as the reduce kernel rounds it
+    const float r = bf16r(bf16_to_f32(xr[i]) + o);
+    xr[i] = f32_to_bf16(r);
+    rowbuf[i] = r;
+    ss = fmaf(r, r, ss);
+  }
+  const float total = block_sum_256(ss, red);
+  const float inv = rsqrtf(total / (float)n + eps);
+  uint16_t* yr = y + row * ldy;
+  for (int i = threadIdx.x; i < n; i += kNormThreads) yr[i] = f32_to_bf16(bf16_to_f32(w[i]) * bf16r(rowbuf[i] * inv));
+}
+
+constexpr int kReduceNormMaxSplits = 16;
+
+template <int S>
+int launch_reduce_norm(int splits, dim3 grid, size_t lds, hipStream_t st, const float* part, const float* scale,
+                       uint16_t* x, int64_t ldx, const uint16_t* w, uint16_t* y, int64_t ldy, int M, int n,
+                       float eps) {
+  if constexpr (S < 2) {
+    return EGPT_ERR_UNSUPPORTED;
+  } else {
+    if (splits != S)
+      return launch_reduce_norm<S - 1>(splits, grid, lds, st, part, scale, x, ldx, w, y, ldy, M, n, eps);
+    hipLaunchKernelGGL(reduce_add_rmsnorm_kernel<S>, grid, dim3(kNormThreads), lds, st, part, scale, x, ldx, w, y,
+                       ldy, M, n, eps);
+    return EGPT_LAUNCH_STATUS();
+  }
+}
+
 }  // namespace
+
+int launch_reduce_add_rmsnorm(const float* part, int splits, const float* scale, void* resid, int64_t ld_resid,
+                              const void* norm_w, void* y, int64_t ldy, int M, int N, float eps, hipStream_t st) {
+  if (!part || !scale || !resid || !norm_w || !y || M < 1 || N < 1 || ld_resid < N || ldy < N)
+    return EGPT_ERR_INVALID;
+  if (splits < 2 || splits > kReduceNormMaxSplits || (size_t)N * sizeof(float) > 64 * 1024)
+    return EGPT_ERR_UNSUPPORTED;
+  return launch_reduce_norm<kReduceNormMaxSplits>(splits, dim3(M), (size_t)N * sizeof(float), st, part, scale,
+                                                  (uint16_t*)resid, ld_resid, (const uint16_t*)norm_w, (uint16_t*)y,
+                                                  ldy, M, N, eps);
+}
+
 }  // namespace egpt
 
 using namespace egpt;

@@ -367,10 +367,39 @@ class Qwen3Int8Engine:
         else:
             int8_gemm(x[:rows], q, s, out=out[:rows])
 
-    def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first, pos0=0):
+    def _linear_add_norm(self, xin, q, s, out, x, norm_w, h, rows):
+        """x = bf16(x + linear(xin)) and h = RMSNorm(x) * norm_w for `rows` rows. Split-K shapes take
+        egpt_int8_gemm_add_rmsnorm (one launch after the split slices instead of the reduce and the norm, the
+        same bits); the others the linear into `out`, then egpt_add_rmsnorm."""
+        lib, c, st = _lib.lib(), self.cfg, self._stream()
+        if rows > MAX_DECODE_ROWS:
+            need = ctypes.c_size_t()
+            _lib.check('egpt_int8_gemm_workspace',
+                       lib.egpt_int8_gemm_workspace(rows, q.shape[0], q.shape[1], ctypes.byref(need)))
+            if need.value:
+                ws = torch.empty(need.value, device=self.device, dtype=torch.uint8)
+                r = lib.egpt_int8_gemm_add_rmsnorm(xin.data_ptr(), xin.stride(0), q.data_ptr(), q.stride(0),
+                                                   s.data_ptr(), x.data_ptr(), x.stride(0), norm_w.data_ptr(),
+                                                   h.data_ptr(), h.stride(0), rows, q.shape[0], q.shape[1], c.rms_eps,
+                                                   ws.data_ptr(), need.value, st)
+                if r != _lib.EGPT_ERR_UNSUPPORTED:
+                    _lib.check('egpt_int8_gemm_add_rmsnorm', r)
+                    return
+        self._linear(xin, q, s, out, rows)
+        _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0),
+                                                            norm_w.data_ptr(), h.data_ptr(), h.stride(0), rows,
+                                                            c.hidden, c.rms_eps, st))
+
+    def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first, pos0=0,
+               normed=False):
+        """One layer over `rows` rows. `normed`: h already holds the layer's input RMSNorm (the previous layer's
+        down projection folded it in); the layer then folds the next layer's input norm into its own down
+        projection when there is a next layer (returns True), and leaves x + down to the caller otherwise."""
         lib, c, L, st = _lib.lib(), self.cfg, self.layers[i], self._stream()
         d = c.head_dim
-        if first:
+        if normed:
+            pass
+        elif first:
             _lib.check('egpt_rmsnorm', lib.egpt_rmsnorm(x.data_ptr(), x.stride(0), L['in_w'].data_ptr(), h.data_ptr(),
                                                         h.stride(0), rows, c.hidden, c.rms_eps, st))
         else:
@@ -393,14 +422,15 @@ class Qwen3Int8Engine:
                 _lib.check('egpt_prefill_attn', st_pf)
         else:
             self._kernel_attention(qrot, kc, vc, rows, positions, pos_stride, attn)
-        self._linear(attn, L['o_q'], L['o_s'], o, rows)
-        _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
-            x.data_ptr(), x.stride(0), o.data_ptr(), o.stride(0), L['post_w'].data_ptr(), h.data_ptr(), h.stride(0),
-            rows, c.hidden, c.rms_eps, st))
+        self._linear_add_norm(attn, L['o_q'], L['o_s'], o, x, L['post_w'], h, rows)
         self._linear(h, L['gu_q'], L['gu_s'], gu, rows)
         _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
                                                       act.stride(0), rows, st))
+        if i + 1 < c.layers and rows > MAX_DECODE_ROWS:  # the next layer's input norm folds into this projection
+            self._linear_add_norm(act, L['down_q'], L['down_s'], down, x, self.layers[i + 1]['in_w'], h, rows)
+            return True
         self._linear(act, L['down_q'], L['down_s'], down, rows)
+        return False
 
     def _kernel_attention(self, qrot, kc, vc, rows, positions, pos_stride, attn):
         """Split-K attention of `rows` query rows over the shared cache (each row a batch row, batch stride 0)."""
@@ -506,8 +536,10 @@ class Qwen3Int8Engine:
         lib = _lib.lib()
         _lib.check('egpt_embed', lib.egpt_embed(ids.data_ptr(), t, self.embed.data_ptr(), self.embed.stride(0),
                                                 c.vocab, x.data_ptr(), x.stride(0), c.hidden, self._stream()))
+        normed = False
         for i in range(c.layers):
-            self._layer(i, t, x, h, qkv, qrot, attn, o, gu, act, down, positions, 1, first=(i == 0), pos0=pos0)
+            normed = self._layer(i, t, x, h, qkv, qrot, attn, o, gu, act, down, positions, 1, first=(i == 0),
+                                 pos0=pos0, normed=normed)
         self.position.fill_(pos0 + t - 1)  # argmax advances it to pos0 + t
         self._head(x[t - 1:], down[t - 1:], h[t - 1:])
         return self.logits[0]

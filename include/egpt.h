@@ -89,6 +89,19 @@ int egpt_int8_gemm_workspace(int M, int N, int K, size_t *bytes);
 int egpt_int8_gemm_ws(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                       void *y, int64_t ldy, int M, int N, int K, void *workspace, size_t workspace_bytes,
                       hipStream_t stream);
+/* The split-K product followed by the residual update and RMSNorm of each output row, the pair that follows
+ * o_proj and down_proj in a prompt pass (transformers' Qwen3 decoder layer, models/qwen3/modeling_qwen3.py:285-322:
+ * residual add, then the next RMSNorm): o = the product above, resid = bf16(resid + o) (written back), y =
+ * RMSNorm(resid) * norm_w (as egpt_add_rmsnorm). The splits' sum, both roundings, the residual and the norm run in
+ * one launch after the split slices, bit-identical to egpt_int8_gemm_ws followed by egpt_add_rmsnorm; o itself is
+ * not stored. Only for shapes that split K (egpt_int8_gemm_workspace > 0, the same workspace) and N <= 16384;
+ * EGPT_ERR_UNSUPPORTED otherwise, before any launch (the caller runs the two calls). Replaces, with
+ * egpt_int8_gemm_ws, the reference's prefill formula (research/realmodel/int8_linear.py:96-97) and the residual +
+ * RMSNorm its Inductor graph fuses after it. */
+int egpt_int8_gemm_add_rmsnorm(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                               void *resid, int64_t ld_resid, const void *norm_w, void *y, int64_t ldy,
+                               int M, int N, int K, float eps, void *workspace, size_t workspace_bytes,
+                               hipStream_t stream);
 
 /*
  * Split-K GQA decode attention (flash decoding) with its partial-softmax reduce.

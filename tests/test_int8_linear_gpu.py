@@ -340,3 +340,43 @@ def test_int8_linear_opcheck(rows):
     w = torch.randint(-127, 128, (512, 2048), generator=g, dtype=torch.int8).cuda()
     s = (torch.rand(512, generator=g) * 0.01 + 1e-3).cuda()
     torch.library.opcheck(torch.ops.efficientgpt.int8_linear.default, (x, w, s))
+
+
+@pytest.mark.parametrize('m,k,n', [(128, 6144, 2048), (128, 2048, 2048), (64, 2048, 2048), (33, 6144, 2048),
+                                   (100, 4096, 1000)])
+def test_gemm_add_rmsnorm_matches_the_two_calls_bit_for_bit(m, k, n):
+    """egpt_int8_gemm_add_rmsnorm (split slices, then one row kernel: the splits' sum, both roundings, the residual
+    and the RMSNorm) against egpt_int8_gemm_ws followed by egpt_add_rmsnorm on the same inputs: residual and norm
+    output bit-identical; too small a workspace and unsplit shapes are refused before any launch."""
+    from efficientgpt_amd import _lib
+    import ctypes
+    lib = _lib.lib()
+    need = ctypes.c_size_t()
+    assert lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(need)) == 0 and need.value > 0
+    x, q, s = make_case(m, k, n, seed=3 * m + n)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    g = torch.Generator().manual_seed(m + k)
+    resid = torch.randn(m, n, generator=g).to(torch.bfloat16).cuda()
+    nw = (1 + 0.1 * torch.randn(n, generator=g)).to(torch.bfloat16).cuda()
+    ws = torch.empty(need.value, device='cuda', dtype=torch.uint8)
+    st = _lib.stream_ptr()
+    # two calls
+    o = torch.empty(m, n, device='cuda', dtype=torch.bfloat16)
+    r2, h2 = resid.clone(), torch.empty(m, n, device='cuda', dtype=torch.bfloat16)
+    assert lib.egpt_int8_gemm_ws(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), o.data_ptr(), n, m, n, k,
+                                 ws.data_ptr(), need.value, st) == 0
+    assert lib.egpt_add_rmsnorm(r2.data_ptr(), n, o.data_ptr(), n, nw.data_ptr(), h2.data_ptr(), n, m, n, 1e-6, st) == 0
+    # one call
+    r1, h1 = resid.clone(), torch.full((m, n), float('nan'), device='cuda', dtype=torch.bfloat16)
+    assert lib.egpt_int8_gemm_add_rmsnorm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), r1.data_ptr(), n,
+                                          nw.data_ptr(), h1.data_ptr(), n, m, n, k, 1e-6, ws.data_ptr(), need.value,
+                                          st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2) and torch.equal(h1, h2)
+    assert not bool(torch.isnan(h1.float()).any())
+    assert lib.egpt_int8_gemm_add_rmsnorm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), r1.data_ptr(), n,
+                                          nw.data_ptr(), h1.data_ptr(), n, m, n, k, 1e-6, ws.data_ptr(),
+                                          need.value - 4, st) == _lib.EGPT_ERR_WORKSPACE
+    assert lib.egpt_int8_gemm_add_rmsnorm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), r1.data_ptr(), n,
+                                          nw.data_ptr(), h1.data_ptr(), n, 1024, n, k, 1e-6, ws.data_ptr(),
+                                          need.value, st) == _lib.EGPT_ERR_UNSUPPORTED  # 1024 rows: K not split
