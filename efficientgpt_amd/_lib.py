@@ -30,6 +30,7 @@ SIGNATURES = {
     'egpt_abi_version': (_c_int, []),
     'egpt_status_string': (ctypes.c_char_p, [_c_int]),
     'egpt_int8_gemv': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp]),
+    'egpt_quantize_rows': (_c_int, [_c_int, _c_vp, _c_i64, _c_int, _c_int, _c_vp, _c_i64, _c_vp, _c_vp]),
     'egpt_int8_gemm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp]),
     'egpt_int8_gemm_workspace': (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
     'egpt_int8_gemm_ws': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,

@@ -6,11 +6,13 @@ implementation), same `int8_matmul`, `quantize_weight`, `Int8Linear` and
 `quantize_model` signatures, buffer names and error messages.
 
 Weights are quantised per output channel, symmetric: s = max|w| / 127,
-q = round(w / s) in [-127, 127] (round half to even). Decode (<= 16 rows) runs the
-HIP GEMV through libegpt_hip.so: fp32 accumulation, scale applied to the finished
-sum, one bf16 rounding. Prefill (> 16 rows) takes the reference's own formula
-`((x @ q.bf16.T).float() * s).bf16` (int8_linear.py:96-97), a plain library GEMM on
-the GPU.
+q = round(w / s) in [-127, 127] (round half to even); device tensors are quantised by
+the HIP kernel egpt_quantize_rows (correctly rounded fp32 steps, the same bits as the
+formula on the CPU). Decode (<= 16 rows) runs the HIP GEMV through libegpt_hip.so:
+fp32 accumulation, scale applied to the finished sum, one bf16 rounding. Prefill
+(> 16 rows) computes the reference's formula `((x @ q.bf16.T).float() * s).bf16`
+(int8_linear.py:96-97) on the MFMA GEMM egpt_int8_gemm, which reads the int8 codes
+directly (no bf16 copy of the weights).
 
 `CONFIGS` / `DEFAULT` keep the reference's tuple format
 (family, BLOCK_N, BLOCK_K, SPLITK, warps) (int8_linear.py:18-23): family
@@ -93,14 +95,14 @@ def int8_linear(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> torch.Tens
     return y.reshape(*x.shape[:-1], w.shape[0])
 
 
-def int8_gemm(x2, w, s, out=None):
+def int8_gemm(x2, w, s, out=None, workspace=None):
     """Prefill rows: bf16(fp32(bf16(x2 @ w^T)) * s), the reference's formula for more than 16 rows
     (research/realmodel/int8_linear.py:96-97), on the MFMA kernel egpt_int8_gemm, which reads the int8 weights
     directly (no bf16 copy of them). Measured on the MI355X against the reference's dequantise-then-library-GEMM
     formula at the Qwen3-1.7B and Qwen3-8B shapes: 1.2-2.9x faster at 128 rows, 1.1-1.4x at 1024-2048, and at
-    8192 rows 0.93-1.4x (faster on 14 of 16 shapes, the whole 8B layer 8% faster). Shapes the kernel does not
-    take (K not a multiple of 64, unaligned rows, operands of 2 GiB or more) run the same formula on the library
-    GEMM as the reference does."""
+    8192 rows 0.93-1.4x (faster on 14 of 16 shapes, the whole 8B layer 8% faster). Shapes the MFMA kernel does
+    not take (K not a multiple of 64, unaligned rows, operands of 2 GiB or more) run the library's generic kernel,
+    the same formula without MFMA."""
     m, k = x2.shape
     n = w.shape[0]
     if x2.stride(1) != 1:
@@ -113,14 +115,14 @@ def int8_gemm(x2, w, s, out=None):
     lib = _lib.lib()
     need = ctypes.c_size_t()
     _lib.check('egpt_int8_gemm_workspace', lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(need)))
-    ws = torch.empty(need.value, device=x2.device, dtype=torch.uint8) if need.value else None
+    ws = None
+    if need.value:  # split K: the caller's workspace when it is large enough, else one from torch's allocator
+        ws = workspace if workspace is not None and workspace.numel() >= need.value else \
+            torch.empty(need.value, device=x2.device, dtype=torch.uint8)
     st = lib.egpt_int8_gemm_ws(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), s.data_ptr(),
                                out.data_ptr(), out.stride(0), m, n, k, ws.data_ptr() if ws is not None else None,
-                               need.value, _lib.stream_ptr(x2.device))
-    if st == _lib.EGPT_ERR_UNSUPPORTED:
-        out.copy_(((x2 @ w.to(torch.bfloat16).t()).float() * s).to(torch.bfloat16))
-    else:
-        _lib.check('egpt_int8_gemm', st)
+                               ws.numel() if ws is not None else 0, _lib.stream_ptr(x2.device))
+    _lib.check('egpt_int8_gemm', st)
     return out
 
 
@@ -140,15 +142,38 @@ def _quantize_rows(rows):
     return codes, step
 
 
+_QUANT_DTYPES = {torch.float32: _lib.EGPT_F32, torch.bfloat16: _lib.EGPT_BF16, torch.float16: _lib.EGPT_F16}
+
+
+def _quantize_on_device(w):
+    """(q, s) of a 2-D device tensor by egpt_quantize_rows: one launch, rows of any stride along dim 0."""
+    if w.dtype not in _QUANT_DTYPES:
+        w = w.float()  # the reference's `.float()` of the weight
+    if w.dim() != 2 or w.shape[1] < 1:
+        raise ValueError(f'quantize_weight expects a 2-D weight with K >= 1, got {tuple(w.shape)}')
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    n, k = w.shape
+    q = torch.empty((n, k), dtype=torch.int8, device=w.device)
+    s = torch.empty(n, dtype=torch.float32, device=w.device)
+    st = _lib.lib().egpt_quantize_rows(_QUANT_DTYPES[w.dtype], w.data_ptr(), w.stride(0), n, k, q.data_ptr(),
+                                       q.stride(0), s.data_ptr(), _lib.stream_ptr(w.device))
+    _lib.check('egpt_quantize_rows', st)
+    return q, s
+
+
 def quantize_weight(weight):
     """Per-output-channel symmetric int8: returns (q int8 [N, K], s fp32 [N]) with weight ~= q * s[:, None].
 
     s = max(max_k |w| / 127, 1e-12) in fp32 and q = clamp(round(w / s), -127, 127)
-    with round half to even (research/realmodel/int8_linear.py:106-117). Every row is
-    independent, so quantising ROW_BLOCK rows at a time gives the same bits as the
-    whole matrix at once.
+    with round half to even (research/realmodel/int8_linear.py:106-117). Device tensors go
+    through the HIP kernel egpt_quantize_rows, whose every step is one correctly rounded
+    fp32 operation. Host tensors take the formula in torch; every row is independent, so
+    quantising ROW_BLOCK rows at a time gives the same bits as the whole matrix at once.
     """
     w = weight.detach()
+    if w.is_cuda:
+        return _quantize_on_device(w)
     q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
     s = torch.empty(w.shape[0], dtype=torch.float32, device=w.device)
     for lo in range(0, w.shape[0], ROW_BLOCK):

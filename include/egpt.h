@@ -65,15 +65,29 @@ int egpt_int8_gemv_splitk(const void *x, int64_t ldx, const int8_t *w, int64_t l
                           void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Per-output-channel symmetric int8 quantisation of a float matrix w [N, K] (row
+ * stride ldw) into codes q int8 [N, K] (row stride ldq) and steps s fp32 [N]:
+ *   s[n]    = max(max_k |w[n, k]| / 127, 1e-12)        (fp32, correctly rounded)
+ *   q[n, k] = clamp(round_half_even(w[n, k] / s[n]), -127, 127)
+ * dtype: EGPT_F32 / EGPT_BF16 / EGPT_F16, converted exactly to fp32 first. Each
+ * step is one correctly rounded fp32 operation, so the bits equal the formula on
+ * the CPU. Codes of rows holding NaN or infinity are unspecified.
+ * Replaces quantize_weight for device tensors (research/realmodel/int8_linear.py:106-117).
+ */
+int egpt_quantize_rows(int dtype, const void *w, int64_t ldw, int N, int K, int8_t *q, int64_t ldq, float *s,
+                       hipStream_t stream);
+
+/*
  * Int8-weight GEMM for prefill (any M, typically > 16 rows):
  *   y[m, n] = bf16( fp32( bf16( sum_k x[m, k] * w[n, k] ) ) * scale[n] )
  * fp32 accumulation on bf16 MFMA with the weights' exact bf16 image, rounded once to
  * bf16, then the scale in fp32 and a second rounding: the reference's prefill formula
  * `((x2 @ w.to(bfloat16).t()).float() * s).to(bfloat16)` (research/realmodel/int8_linear.py:96-97),
  * without materialising the bf16 weights. x bf16 [M, K] (row stride ldx), w int8 [N, K]
- * (ldw), y bf16 [M, N] (ldy). Needs K a multiple of 64, ldx % 8 == 0, ldw % 16 == 0 and
- * 16-byte aligned x and w; returns EGPT_ERR_UNSUPPORTED otherwise (the caller keeps the
- * library formula for such shapes).
+ * (ldw), y bf16 [M, N] (ldy). The MFMA kernel takes K a multiple of 64, ldx % 8 == 0,
+ * ldw % 16 == 0, 16-byte aligned x and w and operands under 2 GiB; any other shape runs
+ * a generic kernel (fp32 sums over lane-strided K, the same two roundings), slower but
+ * with the same contract.
  */
 int egpt_int8_gemm(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                    void *y, int64_t ldy, int M, int N, int K, hipStream_t stream);
@@ -145,7 +159,9 @@ int egpt_decode_attn(int dtype,
  * 16 query heads x 504 splits). The device that runs the call must be current
  * (EGPT_ERR_INVALID if `stream` belongs to another). Calls that overlap on one
  * device share the array and race; the first call on a device looks up the array's
- * address there, so make it before a graph capture.
+ * address there, so make it before a graph capture: made while `stream` is being
+ * captured it returns EGPT_ERR_INVALID and launches nothing. A failed lookup is not
+ * remembered; the next call looks up again.
  */
 #define EGPT_NOALLOC_SCRATCH_BYTES (4u << 20)
 int egpt_decode_attn_noalloc(int dtype,

@@ -54,6 +54,11 @@ def test_argument_errors_return_status_without_launching():
     assert size.value > _lib.NOALLOC_SCRATCH_BYTES
     assert lib.egpt_decode_attn_noalloc(1, *args, 1, 16, 8, 4096, 128, 505, 0.1, None) == -4
     assert lib.egpt_decode_attn_noalloc(1, *args, 0, 16, 8, 4096, 128, 1, 0.1, None) == -1
+    # quantisation: null codes, row stride shorter than K, unknown dtype; no rows is a no-op
+    assert lib.egpt_quantize_rows(0, dummy, 64, 4, 64, None, 64, dummy, None) == -1
+    assert lib.egpt_quantize_rows(0, dummy, 32, 4, 64, dummy, 64, dummy, None) == -1
+    assert lib.egpt_quantize_rows(9, dummy, 64, 4, 64, dummy, 64, dummy, None) == -2
+    assert lib.egpt_quantize_rows(1, dummy, 64, 0, 64, dummy, 64, dummy, None) == 0
 
 
 @pytest.mark.parametrize('b,hkv,cap', [(1, 8, 256), (1, 8, 32768), (16, 6, 128), (1, 1, 1)])

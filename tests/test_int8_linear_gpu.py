@@ -40,8 +40,9 @@ def check_against_oracle(y, x, q, s, min_exact=0.99):
     """Reference tolerance vs fp64 truth, and within one bf16 ulp of the oracle's formula for the row count.
 
     Past 16 rows the op takes the prefill GEMM (the reference's formula, two bf16
-    roundings), and 3-16 rows the small-batch MFMA kernel (one rounding). Their fp32
-    sums over K run in the MFMA order; the oracle sums exactly. An
+    roundings), and up to 16 rows the GEMV kernels (one rounding). Their fp32 sums
+    over K run in the kernels' orders (lane chunks and DPP reductions, or the MFMA's);
+    the oracle sums exactly. An
     fp32 sum of K terms is off by about sqrt(K) 2^-24 sum|x q| (a random-walk bound),
     which near a cancelling zero is many ulps of a tiny output. So there each element
     may differ by that sum error times the scale plus one ulp per rounding (three for
@@ -61,10 +62,8 @@ def check_against_oracle(y, x, q, s, min_exact=0.99):
     sum_err = 2.0 ** -24 * np.sqrt(xn.shape[1]) * sum_abs
     if prefill:
         bound = 3.0 * bf16_ulp(want) + sum_err
-    elif xn.shape[0] > 2:  # 3-16 rows: the MFMA kernel, fp32 sums in the MFMA's order
+    else:  # one rounding of an fp32 sum taken in the kernel's order
         bound = bf16_ulp(want) + sum_err
-    else:
-        bound = bf16_ulp(want)
     assert np.all(diff <= bound), float((diff - bound).max())
     assert np.mean(diff == 0) >= min_exact, float(np.mean(diff == 0))
     rel = np.abs(yn - oint8.linear_truth(xn, qn, sn)).max() / max(np.abs(oint8.linear_truth(xn, qn, sn)).max(), 1e-30)
@@ -91,6 +90,15 @@ def test_gemv_edges(edge):
 def test_lm_head_shape():
     from efficientgpt_amd.int8_linear import int8_linear
     x, q, s = make_case(1, 2048, 151936, seed=11)
+    check_against_oracle(int8_linear(x.cuda(), q.cuda(), s.cuda()), x, q, s)
+
+
+@pytest.mark.parametrize('m', [2, 4, 8])
+def test_lm_head_small_batch(m):
+    """The Qwen3 lm_head (151936 x 2048) at 2, 4 and 8 rows: the few-rows vector kernel at 2 rows, the LDS-staged
+    MFMA form (outputs past 8192 features, K 2048) at 4 and 8."""
+    from efficientgpt_amd.int8_linear import int8_linear
+    x, q, s = make_case(m, 2048, 151936, seed=11 + m)
     check_against_oracle(int8_linear(x.cuda(), q.cuda(), s.cuda()), x, q, s)
 
 
@@ -313,16 +321,30 @@ def test_prefill_gemm_split_k_matches_oracle(m, k, n):
     assert torch.equal(int8_linear(xd, qd, sd), y)
 
 
-def test_prefill_op_uses_kernel_and_falls_back_for_unaligned_k():
+GENERIC_SHAPES = [(40, 100, 70), (17, 2051, 33), (64, 96, 257)]
+
+
+@pytest.mark.parametrize('m,k,n', GENERIC_SHAPES)
+def test_prefill_generic_kernel_for_shapes_the_mfma_kernel_refuses(m, k, n):
+    """K not a multiple of 64, and x rows 6 bytes off 16-byte alignment: egpt_int8_gemm runs its generic
+    kernel (no library formula anywhere in the op) with the prefill formula's two roundings, against the oracle."""
     from efficientgpt_amd import _lib
     from efficientgpt_amd.int8_linear import int8_linear
-    x, q, s = make_case(40, 100, 70, seed=9)  # K = 100: not a multiple of 64
-    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
-    st = _lib.lib().egpt_int8_gemm(xd.data_ptr(), 100, qd.data_ptr(), 100, sd.data_ptr(),
-                                   torch.empty(40, 70, device='cuda', dtype=torch.bfloat16).data_ptr(), 70, 40, 70,
-                                   100, _lib.stream_ptr())
-    assert st == _lib.EGPT_ERR_UNSUPPORTED
-    check_against_oracle(int8_linear(xd, qd, sd).cpu(), x, q, s)
+    x, q, s = make_case(m, k, n, seed=m + k + n)
+    qd, sd = q.cuda(), s.cuda()
+    big = torch.zeros(m, k + 3, dtype=torch.bfloat16)
+    big[:, 3:] = x
+    xd = big.cuda()[:, 3:]  # unaligned rows, row stride k + 3
+    y = torch.full((m, n), float('nan'), device='cuda', dtype=torch.bfloat16)
+    st = _lib.lib().egpt_int8_gemm(xd.data_ptr(), k + 3, qd.data_ptr(), k, sd.data_ptr(), y.data_ptr(), n, m, n, k,
+                                   _lib.stream_ptr())
+    assert st == 0, st
+    check_against_oracle(y.cpu(), x, q, s)
+    assert torch.equal(int8_linear(xd, qd, sd), y)  # the op takes the same kernel
+
+
+def test_prefill_op_keeps_leading_dims():
+    from efficientgpt_amd.int8_linear import int8_linear
     x, q, s = make_case(48, 2048, 512, seed=11)
     y = int8_linear(x.cuda().view(4, 12, 2048), q.cuda(), s.cuda())  # leading dims, kernel path
     assert y.shape == (4, 12, 512)
