@@ -390,6 +390,50 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
   return EGPT_LAUNCH_STATUS();
 }
 
+// The same product for shapes the MFMA kernel does not take (K not a multiple of
+// 64, rows not 16-byte aligned, operands past its 32-bit offsets): one wavefront
+// per output feature n and group of kGenericRows rows, lanes striding K with
+// element loads (any alignment, 64-bit indexing), fp32 sums reduced across the
+// wavefront in a fixed order, then the two roundings of the prefill formula,
+// y = bf16(bf16(sum) * scale[n]). No MFMA and no LDS: a correct form for the
+// odd shapes, not a fast one.
+constexpr int kGenericRows = 4;
+constexpr int kGenericWaves = 4;
+
+__global__ __launch_bounds__(kGenericWaves * kWave) void int8_gemm_generic_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ w, int64_t ldw,
+    const float* __restrict__ scale, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t mgroups = ((int64_t)M + kGenericRows - 1) / kGenericRows;
+  const int64_t wv = (int64_t)blockIdx.x * kGenericWaves + threadIdx.x / kWave;
+  if (wv >= mgroups * N) return;  // wave-uniform
+  const int64_t n = wv / mgroups;  // neighbouring wavefronts share a weight row
+  const int64_t m0 = (wv - n * mgroups) * kGenericRows;
+  const int8_t* wr = w + n * ldw;
+  float acc[kGenericRows] = {};
+  for (int64_t k = lane; k < K; k += kWave) {
+    const float wk = (float)gload(wr + k);
+#pragma unroll
+    for (int r = 0; r < kGenericRows; ++r)
+      if (m0 + r < M) acc[r] = fmaf(bf16_to_f32(gload(x + (m0 + r) * ldx + k)), wk, acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < kGenericRows; ++r) {
+    const float sum = wave_sum(acc[r]);
+    if (lane == r && m0 + r < M) gstore(y + (m0 + r) * ldy + n, f32_to_bf16(bf16_to_f32(f32_to_bf16(sum)) * scale[n]));
+  }
+}
+
+int launch_generic(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, uint16_t* y,
+                   int64_t ldy, int M, int N, int K, hipStream_t st) {
+  const int64_t waves = ((int64_t)M + kGenericRows - 1) / kGenericRows * N;
+  const int64_t blocks = (waves + kGenericWaves - 1) / kGenericWaves;
+  if (blocks > (int64_t)UINT32_MAX) return EGPT_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(int8_gemm_generic_kernel, dim3((unsigned)blocks), dim3(kGenericWaves * kWave), 0, st, x, ldx, w,
+                     ldw, scale, y, ldy, M, N, K);
+  return EGPT_LAUNCH_STATUS();
+}
+
 // K slices for a short-M GEMM whose 64 x 64 tiles leave CUs idle: the fewest
 // (a power of two, at most 16) that give every CU a block, each slice a multiple
 // of kBKSplit and at least 256 wide. 1 when the tiles already fill the chip, or K
@@ -427,13 +471,13 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
   if (!x || !w || !scale || !y || M < 0 || N < 0 || K < 0) return EGPT_ERR_INVALID;
   if (ldx < K || ldw < K || ldy < N) return EGPT_ERR_INVALID;
   if (M == 0 || N == 0) return EGPT_OK;
-  if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
-    return EGPT_ERR_UNSUPPORTED;
-  // the kernel addresses each operand by 32-bit byte offsets
-  if ((int64_t)M * ldx * 2 >= ((int64_t)1 << 31) || (int64_t)N * ldw >= ((int64_t)1 << 31) ||
-      (int64_t)M * ldy * 2 >= ((int64_t)1 << 31))
-    return EGPT_ERR_UNSUPPORTED;
-  if (((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX / kMaxSplits) return EGPT_ERR_UNSUPPORTED;
+  // The MFMA kernel takes K a multiple of 64, 16-byte aligned rows and operands its
+  // 32-bit byte offsets reach; every other shape runs the generic kernel.
+  if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16 ||
+      (int64_t)M * ldx * 2 >= ((int64_t)1 << 31) || (int64_t)N * ldw >= ((int64_t)1 << 31) ||
+      (int64_t)M * ldy * 2 >= ((int64_t)1 << 31) ||
+      ((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX / kMaxSplits)
+    return launch_generic((const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, stream);
   GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0, 1, K, nullptr};
   if (workspace) {  // a workspace lets short-M shapes split K
     int splits, kchunk;

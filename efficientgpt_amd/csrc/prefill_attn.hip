@@ -41,12 +41,10 @@ namespace {
 typedef __bf16 bf16x8_pf __attribute__((ext_vector_type(8)));
 typedef float f32x16_pf __attribute__((ext_vector_type(16)));
 
-constexpr int kPfD = 128;              // head dim
 constexpr int kPfSlots = 64;           // K/V slots per tile
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfStage = kPfThreads / 2;  // threads staging K (and as many staging V)
-constexpr int kPfKRow = kPfD + 8;      // bf16 per K row in LDS (16 bytes of padding)
 constexpr int kPfVRow = kPfSlots + 8;  // bf16 per V^T row in LDS
 constexpr float kPfLog2e = 1.4426950408889634f;
 
@@ -68,7 +66,13 @@ struct PrefillArgs {
 // Position of slot s (0..15 of a 16-slot step) in the staged V^T row: bits 2 and 3 swapped.
 __device__ __forceinline__ int vperm(int s) { return (s & 3) | ((s >> 2 & 1) << 3) | ((s >> 3 & 1) << 2); }
 
+// D: head dim (32, 64 or 128), a multiple of the MFMA's 32 output rows.
+template <int D>
 __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const PrefillArgs a) {
+  constexpr int kPfD = D;
+  constexpr int kPfKRow = kPfD + 8;     // bf16 per K row in LDS (16 bytes of padding)
+  constexpr int kChunks = kPfD / 8;     // 16-byte chunks per K/V row
+  constexpr int kLoads = kChunks / 4;   // 16-byte loads per staging thread and tile: 64 slots x kChunks / 256
   __shared__ __align__(16) uint16_t Ks[2][kPfSlots * kPfKRow];
   __shared__ __align__(16) uint16_t Vs[2][kPfD * kPfVRow];
 
@@ -102,34 +106,45 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
     for (int kk = 0; kk < kPfD / 16; ++kk) qf[kk] = ld16(qrow + 16 * kk);
   }
 
-  // Staging of one K/V tile: 64 slots x 16 chunks of 8 dims each for K and V. The
-  // first 4 wavefronts stage V, the other 4 K, so every thread keeps four 16-byte
-  // loads in flight. A K thread t takes chunks (slot c / 16, chunk c % 16) for c =
-  // t + 256 i; a V thread t takes chunk vc = t % 16 of the four consecutive slots
-  // 4 vg .. 4 vg + 3 (vg = t / 16), whose staged positions are consecutive too
-  // (vperm keeps bits 0 and 1), so each of its 8 dims is one 8-byte LDS store.
+  // Staging of one K/V tile: 64 slots x kChunks chunks of 8 dims each for K and V.
+  // The first 4 wavefronts stage V, the other 4 K, so every thread keeps kLoads
+  // 16-byte loads in flight (4 at D 128). A K thread t takes chunks (slot c /
+  // kChunks, chunk c % kChunks) for c = t + 256 i; a V thread t < 64 kChunks / 4
+  // takes chunk vc = t % kChunks of the four consecutive slots 4 vg .. 4 vg + 3 (vg
+  // = t / kChunks), whose staged positions are consecutive too (vperm keeps bits 0
+  // and 1), so each of its 8 dims is one 8-byte LDS store; at D < 128 the other V
+  // threads stage nothing.
   const uint16_t* kb = a.k + (int64_t)hk * a.c_sh;
   const uint16_t* vb = a.v + (int64_t)hk * a.c_sh;
   const int stid = tid % kPfStage;
   const bool do_k = tid >= kPfStage;  // wave-uniform
-  const int vg = stid / 16, vc = stid % 16;
+  const int vg = stid / kChunks, vc = stid % kChunks;
+  const bool v_stager = vg < kPfSlots / 4;
   u32x4 sr[4];
   auto gload = [&](int j) {
+    if (do_k) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = stid + kPfStage * i;
-      const int64_t s = min((int64_t)j * kPfSlots + (do_k ? c / 16 : 4 * vg + i), last);
-      sr[i] = ld16((do_k ? kb : vb) + s * a.c_sn + (do_k ? c % 16 : vc) * 8);
+      for (int i = 0; i < kLoads; ++i) {
+        const int c = stid + kPfStage * i;
+        const int64_t s = min((int64_t)j * kPfSlots + c / kChunks, last);
+        sr[i] = ld16(kb + s * a.c_sn + (c % kChunks) * 8);
+      }
+    } else if (v_stager) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t s = min((int64_t)j * kPfSlots + 4 * vg + i, last);
+        sr[i] = ld16(vb + s * a.c_sn + vc * 8);
+      }
     }
   };
   auto lstore = [&](int buf) {
     if (do_k) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kLoads; ++i) {
         const int c = stid + kPfStage * i;
-        *(u32x4*)&Ks[buf][(c / 16) * kPfKRow + (c % 16) * 8] = sr[i];
+        *(u32x4*)&Ks[buf][(c / kChunks) * kPfKRow + (c % kChunks) * 8] = sr[i];
       }
-    } else {
+    } else if (v_stager) {
       // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions
       const int p0 = (4 * vg) & ~15;
       const int p = p0 + vperm((4 * vg) & 15);
@@ -267,9 +282,8 @@ extern "C" int egpt_prefill_attn(const void* q, int64_t q_ld, const void* k, con
     return EGPT_ERR_INVALID;
   if (rows == 0) return EGPT_OK;
   if ((int64_t)pos0 + rows > cap) return EGPT_ERR_INVALID;
-  if (D != kPfD) return EGPT_ERR_UNSUPPORTED;
+  if (D != 32 && D != 64 && D != 128) return EGPT_ERR_UNSUPPORTED;
   const int group = Hq / Hkv;
-  if (group != 1 && group != 2 && group != 4 && group != 8) return EGPT_ERR_UNSUPPORTED;
   if (q_ld < (int64_t)Hq * D || o_ld < (int64_t)Hq * D || c_sn < D || c_sh < (int64_t)cap * c_sn) return EGPT_ERR_INVALID;
   if (q_ld % 8 || o_ld % 4 || c_sn % 8 || c_sh % 8 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 ||
       (uintptr_t)out % 8)
@@ -286,11 +300,16 @@ extern "C" int egpt_prefill_attn(const void* q, int64_t q_ld, const void* k, con
   a.rows = rows;
   a.group = group;
   a.pos0 = pos0;
-  a.hb = group < 4 ? group : 4;
+  // query heads per block: the largest of 4, 2, 1 that divides the group
+  a.hb = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
   a.bt = 32 * kPfWaves / a.hb;
   a.ntiles = (rows + a.bt - 1) / a.bt;
   a.scale = scale;
   const dim3 grid((unsigned)(Hkv * (group / a.hb)), (unsigned)a.ntiles);
-  hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kPfThreads), 0, stream, a);
+  switch (D) {
+    case 32: hipLaunchKernelGGL(prefill_attn_kernel<32>, grid, dim3(kPfThreads), 0, stream, a); break;
+    case 64: hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(kPfThreads), 0, stream, a); break;
+    default: hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, dim3(kPfThreads), 0, stream, a); break;
+  }
   return EGPT_LAUNCH_STATUS();
 }

@@ -19,17 +19,54 @@ row holds the same consecutive positions inside the cache and that any mask it i
 given allows exactly slots 0..position; anything else raises ValueError instead of
 attending the wrong slots. The check reads the positions on the host, so it is
 skipped while a graph is being captured (a captured step replays fixed shapes that
-were checked when it ran eagerly).
+were checked when it ran eagerly). Every layer of one forward receives the same
+position_ids tensor, so the host read is made once per forward: the result is kept
+for that tensor object while its contents are unchanged (its version counter).
 
-Prefill (several queries per row) is run as a batch of single queries over the
-same cache (batch stride 0), query t attending to slots 0..position_ids[b, t].
+Several queries per row (a prompt): more than PREFILL_KERNEL_MAX_ROWS bf16 queries
+take the causal prompt-attention kernel (egpt_prefill_attn: query t at position
+pos0 + t attends slots 0..pos0 + t, one pass over the prefix per block of queries);
+fewer, or other dtypes, run as a batch of single queries of the split-K decode
+kernel over the same cache (batch stride 0), query t attending slots
+0..position_ids[b, t].
 """
+
+import weakref
 
 import torch
 
+from . import _lib
 from .decode_attention import _run
 
 NAME = 'egpt_decode'
+# Prompts longer than this take the prompt-attention kernel (the engine's rule, qwen3.PREFILL_KERNEL_MAX_ROWS).
+PREFILL_KERNEL_MAX_ROWS = 64
+
+# The last position_ids / mask that passed the host check: (position_ids ref, its version, mask ref or None, mask
+# version, (B, T, cap), host positions [B, T]).
+_checked = [None]
+
+
+def _cached_positions(position_ids, attention_mask, key):
+    c = _checked[0]
+    if c is None or position_ids is None:
+        return None
+    pref, pver, mref, mver, ckey, p = c
+    if pref() is not position_ids or position_ids._version != pver or ckey != key:
+        return None
+    if attention_mask is None:
+        return p if mref is None else None
+    if mref is None or mref() is not attention_mask or attention_mask._version != mver:
+        return None
+    return p
+
+
+def _remember(position_ids, attention_mask, key, p):
+    if position_ids is None:
+        return
+    mref = None if attention_mask is None else weakref.ref(attention_mask)
+    mver = None if attention_mask is None else attention_mask._version
+    _checked[0] = (weakref.ref(position_ids), position_ids._version, mref, mver, key, p)
 
 
 def query_slots(query, key, attention_mask=None, position_ids=None):
@@ -38,15 +75,28 @@ def query_slots(query, key, attention_mask=None, position_ids=None):
     Raises ValueError when the positions or the mask do not describe a causal prefix of the cache: rows at
     different positions (a padded batch), positions that are not consecutive within a row, positions outside
     the cache, or a mask that hides a slot at or before a query's own or shows one after it."""
+    pos, _ = _query_slots(query, key, attention_mask, position_ids)
+    return pos
+
+
+def _query_slots(query, key, attention_mask, position_ids):
+    """(device positions [B, T], host positions [B, T] or None while a graph is being captured)."""
     b, _, t, _ = query.shape
     cap = key.shape[2]
     if position_ids is None:  # no positions: the queries are the last T slots of the cache
         pos = torch.arange(cap - t, cap, device=query.device).expand(b, t)
+        p = torch.arange(cap - t, cap).expand(b, t)
     else:
         pos = position_ids.to(torch.long).expand(b, t)
+        p = None
     if query.is_cuda and torch.cuda.is_current_stream_capturing():
-        return pos
-    p = pos.cpu()
+        return pos, None
+    shape_key = (b, t, cap)
+    cached = _cached_positions(position_ids, attention_mask, shape_key)
+    if cached is not None:
+        return pos, cached
+    if p is None:
+        p = pos.cpu()
     if bool((p != p[:1]).any()):
         raise ValueError('egpt_decode attention: the rows of the batch sit at different positions (a padded '
                          'batch); it reads cache slots 0..position and cannot mask padding: use sdpa for padded '
@@ -65,17 +115,42 @@ def query_slots(query, key, attention_mask=None, position_ids=None):
         if not bool((allowed == want).all()):
             raise ValueError('egpt_decode attention: the attention mask is not the causal prefix 0..position of '
                              'every query (padding or a custom mask); use sdpa for such masks')
-    return pos
+    _remember(position_ids, attention_mask, shape_key, p)
+    return pos, p
+
+
+def _prompt_rows(query, key, value, row, pos0, scale):
+    """Attention of row `row`'s T queries at positions pos0.. on the prompt kernel: [T, Hq, D], or None when the
+    kernel does not take the operands (then the caller runs the decode kernel)."""
+    _, hq, t, d = query.shape
+    _, hkv, cap, _ = key.shape
+    q = query[row].transpose(0, 1).contiguous()  # [T, Hq, D]
+    k, v = key[row], value[row]
+    if k.stride(2) != 1 or v.stride() != k.stride():
+        return None
+    out = torch.empty_like(q)
+    st = _lib.lib().egpt_prefill_attn(q.data_ptr(), hq * d, k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+                                      out.data_ptr(), hq * d, t, hq, hkv, d, cap, pos0, scale,
+                                      _lib.stream_ptr(q.device))
+    if st == _lib.EGPT_ERR_UNSUPPORTED:
+        return None
+    _lib.check('egpt_prefill_attn', st)
+    return out
 
 
 def egpt_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, position_ids=None,
                    **kwargs):
     """query [B, Hq, T, D], key/value [B, Hkv, L, D] -> ([B, T, Hq, D], None)."""
     b, hq, t, d = query.shape
-    pos_all = query_slots(query, key, attention_mask, position_ids)
+    pos_all, host = _query_slots(query, key, attention_mask, position_ids)
     scale = scaling if scaling is not None else d ** -0.5
     outs = []
     for row in range(b):
+        if t > PREFILL_KERNEL_MAX_ROWS and host is not None and query.dtype == torch.bfloat16:
+            o = _prompt_rows(query, key, value, row, int(host[row, 0]), scale)
+            if o is not None:
+                outs.append(o)
+                continue
         q = query[row].transpose(0, 1).unsqueeze(2)  # [T, Hq, 1, D]
         k = key[row:row + 1].expand(t, -1, -1, -1)  # stride-0 batch over one cache row
         v = value[row:row + 1].expand(t, -1, -1, -1)

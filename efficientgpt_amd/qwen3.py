@@ -37,9 +37,13 @@ import torch
 from . import _lib
 from .int8_linear import MAX_DECODE_ROWS, int8_gemm, quantize_weight
 
-# Prompts longer than this take the causal prefill attention (egpt_prefill_attn; the library-GEMM form for head
-# dims it does not take) instead of the split-K decode kernel, which would rescan the prefix once per query row.
+# Prompts longer than this take the causal prefill attention (egpt_prefill_attn) instead of the split-K decode
+# kernel, which would rescan the prefix once per query row.
 PREFILL_KERNEL_MAX_ROWS = 64
+
+# Head geometry the decode-step attention kernels take (egpt_qwen3_decode_step, egpt_decode_attn).
+SUPPORTED_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_GROUPS = (1, 2, 4, 8)
 
 LINEARS = ('self_attn.q_proj', 'self_attn.k_proj', 'self_attn.v_proj', 'self_attn.o_proj',
            'mlp.gate_proj', 'mlp.up_proj', 'mlp.down_proj')
@@ -181,6 +185,10 @@ class Qwen3Int8Engine:
     def __init__(self, cfg, weights, max_cache_len, device='cuda', inv_freq=None, packed=False):
         if max_cache_len < 1:
             raise ValueError('max_cache_len must be >= 1')
+        if cfg.head_dim not in SUPPORTED_HEAD_DIMS or cfg.heads % cfg.kv_heads or \
+                cfg.heads // cfg.kv_heads not in SUPPORTED_GROUPS:
+            raise ValueError(f'head_dim {cfg.head_dim} with {cfg.heads} / {cfg.kv_heads} heads: the attention kernels '
+                             f'take head dims {SUPPORTED_HEAD_DIMS} and {SUPPORTED_GROUPS} query heads per kv head')
         self.cfg = cfg
         self.device = torch.device(device)
         dev, bf = self.device, torch.bfloat16
@@ -190,6 +198,10 @@ class Qwen3Int8Engine:
         def put(t, dtype=None):
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
 
+        # Prompt passes fold the residual add + RMSNorm after o_proj and down_proj into the split-K GEMM's reduce
+        # (egpt_int8_gemm_add_rmsnorm) and the next layer's input norm into the down projection; False runs the
+        # separate linear and egpt_add_rmsnorm calls instead (the same bits).
+        self.fold_norms = True
         pk = weights if packed else pack_qwen3(c, weights)
         check_packed(c, pk)
         self.layers = [{k: put(v) for k, v in L.items()} for L in pk['layers']]
@@ -244,6 +256,7 @@ class Qwen3Int8Engine:
         other.cfg, other.device, other.n_qkv = self.cfg, self.device, self.n_qkv
         other.layers, other.embed, other.norm_w = self.layers, self.embed, self.norm_w
         other.head_q, other.head_s, other.inv_freq = self.head_q, self.head_s, self.inv_freq
+        other.fold_norms = self.fold_norms
         if hasattr(self, 'weights'):
             other.weights = self.weights
         other._init_state(int(max_cache_len))
@@ -357,44 +370,59 @@ class Qwen3Int8Engine:
     def _stream(self):
         return _lib.stream_ptr(self.device)
 
-    def _linear(self, x, q, s, out, rows):
+    def _prefill_workspace(self, rows):
+        """One split-K workspace for a prompt pass of `rows` rows: the largest any of the layer's linears (and
+        their fused reduce) needs at that row count, allocated once per pass and shared by every GEMM of it
+        (the calls run in stream order, so none overlaps another)."""
+        lib, c = _lib.lib(), self.cfg
+        d = c.head_dim
+        need, most = ctypes.c_size_t(), 0
+        for n, k in ((self.n_qkv, c.hidden), (c.hidden, c.heads * d), (2 * c.inter, c.hidden), (c.hidden, c.inter)):
+            _lib.check('egpt_int8_gemm_workspace', lib.egpt_int8_gemm_workspace(rows, n, k, ctypes.byref(need)))
+            most = max(most, need.value)
+        return torch.empty(most, device=self.device, dtype=torch.uint8) if most else None
+
+    def _linear(self, x, q, s, out, rows, ws=None):
         """out[:rows] = int8 linear of x[:rows]; the reference's row rule (<= 16 rows: GEMV kernel, more: the
-        prefill GEMM)."""
+        prefill GEMM, splitting K through `ws` when given)."""
         if rows <= MAX_DECODE_ROWS:
             _lib.check('egpt_int8_gemv', _lib.lib().egpt_int8_gemv(
                 x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), s.data_ptr(), out.data_ptr(), out.stride(0),
                 rows, q.shape[0], q.shape[1], self._stream()))
         else:
-            int8_gemm(x[:rows], q, s, out=out[:rows])
+            int8_gemm(x[:rows], q, s, out=out[:rows], workspace=ws)
 
-    def _linear_add_norm(self, xin, q, s, out, x, norm_w, h, rows):
+    def _linear_add_norm(self, xin, q, s, out, x, norm_w, h, rows, ws=None):
         """x = bf16(x + linear(xin)) and h = RMSNorm(x) * norm_w for `rows` rows. Split-K shapes take
         egpt_int8_gemm_add_rmsnorm (one launch after the split slices instead of the reduce and the norm, the
-        same bits); the others the linear into `out`, then egpt_add_rmsnorm."""
+        same bits); the others, or every shape when `fold_norms` is off, the linear into `out`, then
+        egpt_add_rmsnorm."""
         lib, c, st = _lib.lib(), self.cfg, self._stream()
-        if rows > MAX_DECODE_ROWS:
+        if rows > MAX_DECODE_ROWS and self.fold_norms:
             need = ctypes.c_size_t()
             _lib.check('egpt_int8_gemm_workspace',
                        lib.egpt_int8_gemm_workspace(rows, q.shape[0], q.shape[1], ctypes.byref(need)))
             if need.value:
-                ws = torch.empty(need.value, device=self.device, dtype=torch.uint8)
+                if ws is None or ws.numel() < need.value:
+                    ws = torch.empty(need.value, device=self.device, dtype=torch.uint8)
                 r = lib.egpt_int8_gemm_add_rmsnorm(xin.data_ptr(), xin.stride(0), q.data_ptr(), q.stride(0),
                                                    s.data_ptr(), x.data_ptr(), x.stride(0), norm_w.data_ptr(),
                                                    h.data_ptr(), h.stride(0), rows, q.shape[0], q.shape[1], c.rms_eps,
-                                                   ws.data_ptr(), need.value, st)
+                                                   ws.data_ptr(), ws.numel(), st)
                 if r != _lib.EGPT_ERR_UNSUPPORTED:
                     _lib.check('egpt_int8_gemm_add_rmsnorm', r)
                     return
-        self._linear(xin, q, s, out, rows)
+        self._linear(xin, q, s, out, rows, ws)
         _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0),
                                                             norm_w.data_ptr(), h.data_ptr(), h.stride(0), rows,
                                                             c.hidden, c.rms_eps, st))
 
     def _layer(self, i, rows, x, h, qkv, qrot, attn, o, gu, act, down, positions, pos_stride, first, pos0=0,
-               normed=False):
+               normed=False, ws=None):
         """One layer over `rows` rows. `normed`: h already holds the layer's input RMSNorm (the previous layer's
         down projection folded it in); the layer then folds the next layer's input norm into its own down
-        projection when there is a next layer (returns True), and leaves x + down to the caller otherwise."""
+        projection when there is a next layer (returns True), and leaves x + down to the caller otherwise. `ws`:
+        the pass's split-K workspace (_prefill_workspace)."""
         lib, c, L, st = _lib.lib(), self.cfg, self.layers[i], self._stream()
         d = c.head_dim
         if normed:
@@ -406,30 +434,27 @@ class Qwen3Int8Engine:
             _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
                 x.data_ptr(), x.stride(0), down.data_ptr(), down.stride(0), L['in_w'].data_ptr(), h.data_ptr(),
                 h.stride(0), rows, c.hidden, c.rms_eps, st))
-        self._linear(h, L['qkv_q'], L['qkv_s'], qkv, rows)
+        self._linear(h, L['qkv_q'], L['qkv_s'], qkv, rows, ws)
         kc, vc = self.k_cache[i], self.v_cache[i]
         _lib.check('egpt_qk_norm_rope', lib.egpt_qk_norm_rope(
             qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), L['qn_w'].data_ptr(), L['kn_w'].data_ptr(),
             self.cos.data_ptr(), self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(),
             kc.stride(0), kc.stride(1), rows, c.heads, c.kv_heads, d, self.cap, c.rms_eps, st))
         if rows > PREFILL_KERNEL_MAX_ROWS:
-            st_pf = lib.egpt_prefill_attn(qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(), kc.stride(0),
-                                          kc.stride(1), attn.data_ptr(), attn.stride(0), rows, c.heads, c.kv_heads, d,
-                                          self.cap, pos0, d ** -0.5, st)
-            if st_pf == _lib.EGPT_ERR_UNSUPPORTED:  # head dim other than 128
-                self._prefill_attention(qrot, kc, vc, rows, pos0, attn)
-            else:
-                _lib.check('egpt_prefill_attn', st_pf)
+            _lib.check('egpt_prefill_attn', lib.egpt_prefill_attn(
+                qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+                attn.data_ptr(), attn.stride(0), rows, c.heads, c.kv_heads, d, self.cap, pos0, d ** -0.5, st))
         else:
             self._kernel_attention(qrot, kc, vc, rows, positions, pos_stride, attn)
-        self._linear_add_norm(attn, L['o_q'], L['o_s'], o, x, L['post_w'], h, rows)
-        self._linear(h, L['gu_q'], L['gu_s'], gu, rows)
+        self._linear_add_norm(attn, L['o_q'], L['o_s'], o, x, L['post_w'], h, rows, ws)
+        self._linear(h, L['gu_q'], L['gu_s'], gu, rows, ws)
         _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
                                                       act.stride(0), rows, st))
-        if i + 1 < c.layers and rows > MAX_DECODE_ROWS:  # the next layer's input norm folds into this projection
-            self._linear_add_norm(act, L['down_q'], L['down_s'], down, x, self.layers[i + 1]['in_w'], h, rows)
+        if i + 1 < c.layers and rows > MAX_DECODE_ROWS and self.fold_norms:
+            # the next layer's input norm folds into this projection
+            self._linear_add_norm(act, L['down_q'], L['down_s'], down, x, self.layers[i + 1]['in_w'], h, rows, ws)
             return True
-        self._linear(act, L['down_q'], L['down_s'], down, rows)
+        self._linear(act, L['down_q'], L['down_s'], down, rows, ws)
         return False
 
     def _kernel_attention(self, qrot, kc, vc, rows, positions, pos_stride, attn):
@@ -451,26 +476,6 @@ class Qwen3Int8Engine:
             positions.data_ptr(), pos_stride,
             attn.data_ptr(), attn.stride(0), d,
             ws.data_ptr(), ws.numel(), rows, c.heads, c.kv_heads, self.cap, d, nsplit, d ** -0.5, st))
-
-    @torch.inference_mode()
-    def _prefill_attention(self, qrot, kc, vc, rows, pos0, attn, chunk=1024):
-        """Causal attention of a long prompt in fp32 on the library GEMM (the decode kernel would rescan the
-        prefix once per query row). Query t at position pos0 + t attends to slots 0..pos0 + t."""
-        c = self.cfg
-        d, g = c.head_dim, c.heads // c.kv_heads
-        n = pos0 + rows
-        kt = kc[:, :n].float().transpose(1, 2).contiguous()  # [Hkv, D, n]
-        v = vc[:, :n].float().contiguous()  # [Hkv, n, D]
-        slots = torch.arange(n, device=self.device)
-        for r0 in range(0, rows, chunk):
-            r1 = min(rows, r0 + chunk)
-            cr = r1 - r0
-            q = qrot[r0:r1].view(cr, c.kv_heads, g, d).permute(1, 2, 0, 3).reshape(c.kv_heads, g * cr, d).float()
-            s = torch.matmul(q.contiguous(), kt) * (d ** -0.5)  # [Hkv, g*cr, n]
-            qpos = (pos0 + r0 + torch.arange(cr, device=self.device)).repeat(g)
-            s.masked_fill_(slots[None, None, :] > qpos[None, :, None], float('-inf'))
-            o = torch.matmul(torch.softmax(s, dim=-1), v)  # [Hkv, g*cr, D]
-            attn[r0:r1] = o.view(c.kv_heads, g, cr, d).permute(2, 0, 1, 3).reshape(cr, c.heads * d).to(attn.dtype)
 
     def _head(self, x, down, h):
         """Final residual add + norm of one row, lm_head GEMV, argmax into token, position += 1."""
@@ -536,10 +541,11 @@ class Qwen3Int8Engine:
         lib = _lib.lib()
         _lib.check('egpt_embed', lib.egpt_embed(ids.data_ptr(), t, self.embed.data_ptr(), self.embed.stride(0),
                                                 c.vocab, x.data_ptr(), x.stride(0), c.hidden, self._stream()))
+        ws = self._prefill_workspace(t) if t > MAX_DECODE_ROWS else None
         normed = False
         for i in range(c.layers):
             normed = self._layer(i, t, x, h, qkv, qrot, attn, o, gu, act, down, positions, 1, first=(i == 0),
-                                 pos0=pos0, normed=normed)
+                                 pos0=pos0, normed=normed, ws=ws)
         self.position.fill_(pos0 + t - 1)  # argmax advances it to pos0 + t
         self._head(x[t - 1:], down[t - 1:], h[t - 1:])
         return self.logits[0]

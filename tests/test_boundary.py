@@ -113,3 +113,21 @@ def test_hf_adapter_refuses_padded_batches_and_foreign_masks():
         hf.query_slots(q, k, hidden, torch.tensor([[5]]))
     with pytest.raises(ValueError, match='causal prefix'):
         hf.query_slots(q, k, allowed, torch.tensor([[4]]))
+
+
+def test_hf_adapter_checks_each_position_tensor_once_and_rechecks_changes():
+    """Every layer of a forward passes the same position_ids tensor: the host check runs for the first layer and is
+    reused while that tensor is unchanged (no host read per layer); writing into it, or another mask, checks again."""
+    q, k = _qk(1, 3, 16)
+    pos = torch.arange(4, 7)[None]
+    assert hf.query_slots(q, k, None, pos).tolist() == [[4, 5, 6]]
+    ref, ver = hf._checked[0][0], hf._checked[0][1]
+    assert ref() is pos and ver == pos._version
+    assert hf._cached_positions(pos, None, (1, 3, 16)) is not None
+    assert hf._cached_positions(pos.clone(), None, (1, 3, 16)) is None  # another tensor object: checked again
+    assert hf._cached_positions(pos, None, (1, 3, 17)) is None  # another cache size
+    allowed = torch.ones(1, 1, 3, 16, dtype=torch.bool)
+    assert hf._cached_positions(pos, allowed, (1, 3, 16)) is None  # a mask that was not checked
+    pos[0, 0] = 0  # written in place: its version moves, so the padded positions are caught
+    with pytest.raises(ValueError, match='consecutive'):
+        hf.query_slots(q, k, None, pos)

@@ -7,7 +7,8 @@ bf16 before they multiply v; this kernel does the same. The error budget is
 therefore that rounding plus the output's: with |dp| <= 2^-9 p per probability and
 sum p / l = 1, |d out| <= 2^-9 max|v| + 2^-9 |out| <= 2^-8 max|v| (fp32 logits and
 sums add far less). Each case must meet that bound and the 2e-2 relative bar.
-Query heads per kv head 1, 2, 4 and 8; prompts that start at slot 0 and ones that
+Query heads per kv head 1, 2, 4 and 8 (and 3 and 6, which take blocks of 1 and 2
+query heads); head dims 128, 64 and 32; prompts that start at slot 0 and ones that
 continue a filled cache; strided rows; NaN in every slot past the block, which must
 leave the output bit-identical; logits scaled x8.
 """
@@ -24,7 +25,7 @@ pytestmark = pytest.mark.gpu
 D = 128
 
 
-def _case(rows, hq, hkv, cap, pos0, seed, scale=1.0, q_pad=0, o_pad=0):
+def _case(rows, hq, hkv, cap, pos0, seed, scale=1.0, q_pad=0, o_pad=0, D=D):
     g = torch.Generator().manual_seed(seed)
     q = (torch.randn(rows, hq * D + q_pad, generator=g) * scale).to(torch.bfloat16)
     k = (torch.randn(hkv, cap, D, generator=g) * scale).to(torch.bfloat16)
@@ -33,7 +34,7 @@ def _case(rows, hq, hkv, cap, pos0, seed, scale=1.0, q_pad=0, o_pad=0):
 
 
 def _run(q, k, v, hq, hkv, pos0, o_pad=0):
-    rows, cap = q.shape[0], k.shape[1]
+    rows, cap, D = q.shape[0], k.shape[1], k.shape[2]
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     out = torch.full((rows, hq * D + o_pad), 7.0, dtype=torch.bfloat16, device='cuda')
     st = _lib.lib().egpt_prefill_attn(qd.data_ptr(), qd.stride(0), kd.data_ptr(), vd.data_ptr(), kd.stride(0),
@@ -45,7 +46,7 @@ def _run(q, k, v, hq, hkv, pos0, o_pad=0):
 
 
 def _check(q, k, v, hq, hkv, pos0, o_pad=0):
-    rows = q.shape[0]
+    rows, D = q.shape[0], k.shape[2]
     out = _run(q, k, v, hq, hkv, pos0, o_pad)
     if o_pad:  # columns past the heads are never written
         assert torch.equal(out[:, hq * D:], torch.full((rows, o_pad), 7.0, dtype=torch.bfloat16))
@@ -63,6 +64,15 @@ def _check(q, k, v, hq, hkv, pos0, o_pad=0):
 @pytest.mark.parametrize('rows,cap,pos0', [(67, 80, 0), (300, 320, 0), (130, 200, 37), (1, 16, 0), (129, 700, 500)])
 def test_prefill_attention_matches_fp64(hq, hkv, rows, cap, pos0):
     q, k, v, _ = _case(rows, hq, hkv, cap, pos0, seed=rows + hq)
+    _check(q, k, v, hq, hkv, pos0)
+
+
+@pytest.mark.parametrize('d', [32, 64])
+@pytest.mark.parametrize('hq,hkv', [(4, 2), (6, 6), (12, 4), (12, 2)])
+@pytest.mark.parametrize('rows,cap,pos0', [(100, 128, 0), (130, 200, 37), (1, 16, 0)])
+def test_prefill_attention_small_head_dims_and_any_group(d, hq, hkv, rows, cap, pos0):
+    """Head dims 32 and 64 (the tiny test models and MHA 6 x 64), and groups of 3 and 6 query heads per kv head."""
+    q, k, v, _ = _case(rows, hq, hkv, cap, pos0, seed=rows + hq + d, D=d)
     _check(q, k, v, hq, hkv, pos0)
 
 
@@ -102,8 +112,8 @@ def test_prefill_attention_refuses_what_it_does_not_take():
                                      kv.stride(1), out.data_ptr(), out.stride(0), rows, hq, hkv, d, cap, pos0,
                                      0.1, _lib.stream_ptr())
     assert call() == _lib.EGPT_OK
-    assert call(d=64) == _lib.EGPT_ERR_UNSUPPORTED
-    assert call(hq=24, hkv=8) == _lib.EGPT_ERR_UNSUPPORTED  # 3 query heads per kv head
+    assert call(d=96) == _lib.EGPT_ERR_UNSUPPORTED
+    assert call(hq=12, hkv=8) < 0  # query heads not a multiple of the kv heads
     assert call(pos0=29) < 0 and call(pos0=29) != _lib.EGPT_ERR_UNSUPPORTED  # pos0 + rows past the cache
     assert call(rows=0) == _lib.EGPT_OK
     assert lib.egpt_prefill_attn(q.data_ptr(), q.stride(0), kv.data_ptr(), kv.data_ptr(), kv.stride(0), kv.stride(1),

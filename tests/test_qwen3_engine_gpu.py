@@ -140,6 +140,28 @@ def test_fused_step_matches_unfused_step(shape, std, cap, plen):
     assert agree >= 11, (tu, tf)
 
 
+@pytest.mark.parametrize('shape', [SMALL, SMALL8])
+@pytest.mark.parametrize('plen', [40, 128])
+def test_prefill_folded_norms_equal_separate_calls(shape, plen):
+    """Prompts of 17-128 rows take the split-K GEMM for o_proj and down_proj, with the residual add + RMSNorm folded
+    into its reduce (egpt_int8_gemm_add_rmsnorm) and each down projection also taking the next layer's input norm
+    (the first layer normalises its embedding rows itself; the last leaves x + down to the head). The same prompt
+    with the folds turned off (separate linear and egpt_add_rmsnorm calls, each layer normalising its own input)
+    must give the same logits and the same K/V caches, bit for bit."""
+    eng, _ = build(shape, seed=9, std=0.15, cap=160)
+    prompt = torch.randint(0, shape.vocab, (plen,), generator=torch.Generator().manual_seed(plen))
+    out = []
+    for fold in (True, False):
+        eng.fold_norms = fold
+        eng.reset()
+        logits = eng.prefill(prompt).clone()
+        out.append((logits, eng.k_cache.clone(), eng.v_cache.clone(), int(eng.token), int(eng.position)))
+    (la, ka, va, ta, pa), (lb, kb, vb, tb, pb) = out
+    assert torch.equal(la, lb)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    assert (ta, pa) == (tb, pb) and pa == plen
+
+
 def test_qwen3_1p7b_widths_match_oracle():
     """Real Qwen3-1.7B widths (hidden 2048, inter 6144, vocab 151936, 16/8 heads) at two layers:
     prefill logits and teacher-forced greedy steps of the fused step against the CPU oracle."""
@@ -338,7 +360,8 @@ def test_transformers_model_int8_through_graph_decoder():
 
 
 def test_hf_attention_adapter_matches_oracle_attention():
-    """transformers with attn_implementation 'egpt_decode' (the HIP kernel) vs the fp32 oracle attention."""
+    """transformers with attn_implementation 'egpt_decode' (the HIP kernel) vs the fp32 oracle attention. The
+    100-token prompt is past PREFILL_KERNEL_MAX_ROWS: its prefill runs the prompt-attention kernel at head dim 32."""
     transformers = pytest.importorskip('transformers')
     from efficientgpt_amd import hf
     hf.register()
@@ -352,7 +375,7 @@ def test_hf_attention_adapter_matches_oracle_attention():
     orc = Qwen3Oracle(TINY, sd, dtype=torch.bfloat16, cap=128, inv_freq=model.model.rotary_emb.inv_freq)
     model = model.cuda()
     g = torch.Generator().manual_seed(4)
-    for p in (1, 6, 30):
+    for p in (1, 6, 30, 100):
         x = torch.randint(0, 512, (1, p), generator=g)
         with torch.no_grad():
             got = model.generate(input_ids=x.cuda(), attention_mask=torch.ones_like(x).cuda(), max_new_tokens=20,
