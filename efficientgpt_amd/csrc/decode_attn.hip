@@ -251,11 +251,14 @@ namespace {
 static __device__ __align__(256) unsigned char scratch[EGPT_NOALLOC_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_err[kMaxDevices];
+std::mutex g_scratch_mutex[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];  // set only by a lookup that succeeded
 
-// The scratch array's address on the current device, looked up on its first use there.
+// The scratch array's address on the current device, looked up on its first
+// successful use there. A failed lookup is not kept: the next call tries again.
+// The first lookup on a device is refused while the stream is being captured
+// (the lookup is a runtime call that a capture may not allow); once the address
+// is known, captured calls need no runtime call at all.
 int scratch_on_current_device(hipStream_t stream, void** ptr) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) return EGPT_ERR_LAUNCH;
@@ -265,12 +268,15 @@ int scratch_on_current_device(hipStream_t stream, void** ptr) {
     if (hipStreamGetDevice(stream, &sdev) != hipSuccess) return EGPT_ERR_INVALID;
     if (sdev != dev) return EGPT_ERR_INVALID;  // the array's address is per device: launch with its device current
   }
-  std::call_once(g_scratch_once[dev], [dev] {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex[dev]);
+  if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return EGPT_ERR_LAUNCH;
+    if (cap != hipStreamCaptureStatusNone) return EGPT_ERR_INVALID;  // make one call outside the capture first
     void* p = nullptr;
-    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return EGPT_ERR_LAUNCH;
     g_scratch_ptr[dev] = p;
-  });
-  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev]) return EGPT_ERR_LAUNCH;
+  }
   *ptr = g_scratch_ptr[dev];
   return EGPT_OK;
 }
