@@ -10,7 +10,10 @@ is prefilled, then each step is one replay of the captured decode graph
 Weights, cache and prompt are resident in HBM before timing starts.
 
 Prints one JSON line:
-  value           decode tokens/s over the timed steps (back-to-back graph replays)
+  value           decode tokens/s over K back-to-back graph replays: the median of --rounds
+                  rounds (5), each from the state the prefill left; `spread` holds every
+                  round, the min and max, and the GPU's busy percentage read before timing
+                  (`contended` when above 10%); `host_cpu` the CPU model from /proc/cpuinfo
   roofline        the dominant kernel, the fused int8 GEMV (fused_gemv_kernel): the
                   step's own GEMV launches (egpt_qwen3_step_gemvs, 4 per layer + the
                   lm_head) replayed as one graph through egpt_int8_gemv_fused and timed
@@ -63,6 +66,8 @@ def parse():
     ap.add_argument('--model', choices=('qwen3-1.7b', 'qwen3-8b'), default='qwen3-1.7b')
     ap.add_argument('--prompt', type=int, default=128)
     ap.add_argument('--seed', type=int, default=0)
+    ap.add_argument('--rounds', type=int, default=5,
+                    help='timed rounds of the same K steps; value is the median round (min and max reported)')
     ap.add_argument('--cpu-tokens', type=int, default=256,
                     help='greedy tokens of the CPU baseline (0: skip; the default 256 is the whole decode of the workload)')
     ap.add_argument('--cpu-long-tokens', type=int, default=4,
@@ -399,7 +404,7 @@ def cpu_long_context(cfg, weights, prompt_len, n_tokens, threads, seed=5):
                        f'before timing): {n_tokens} greedy decode steps from position {prompt_len} over a cache whose '
                        f'{prompt_len} slots hold seeded N(0, 1) keys and values (the prefill is not run on the CPU); '
                        f'{dt:.1f} s'),
-            'cpu': platform.processor() or platform.machine()}
+            'cpu': cpu_name()}
 
 
 def long_context(prompt_len=8192, steps=32, warmup=4, seed=0, cpu_tokens=0):
@@ -516,6 +521,32 @@ def copy_bandwidth(nbytes=1 << 30, reps=10):
     return round(2 * nbytes / s / 1e9, 1)  # bytes read + bytes written
 
 
+def cpu_name():
+    """The host CPU's model name from /proc/cpuinfo, as the reference's environment record reads it
+    (research/release/collect_env.py:40-45); the platform's processor string where that file has none."""
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def gpu_busy_percent():
+    """The GPU's busy percentage from the amdgpu driver (sysfs gpu_busy_percent of the device torch runs on), read
+    before timing as the reference reads nvidia-smi's utilisation (research/realmodel/bench_int8.py:46-51); None
+    where the file is not readable."""
+    try:
+        props = torch.cuda.get_device_properties(torch.cuda.current_device())
+        bus = f'{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}.0'
+        with open(f'/sys/bus/pci/devices/{bus}/gpu_busy_percent') as f:
+            return float(f.read().strip())
+    except (OSError, AttributeError, ValueError):
+        return None
+
+
 def host_threads():
     """CPU threads this process may use: OMP_NUM_THREADS if set, else the cores in its affinity mask."""
     env = os.environ.get('OMP_NUM_THREADS')
@@ -612,7 +643,7 @@ def cpu_baseline(eng, prompt, n_tokens, gpu_tokens):
                        f'{t_first - t0:.2f} s), then {n_tokens} greedy tokens in {t1 - t0:.1f} s; decode tok/s = '
                        f'(n-1)/(total-TTFT)'),
             'ttft_s': round(t_first - t0, 3), 'total_s': round(t1 - t0, 3), 'tokens': n_tokens,
-            'cpu': platform.processor() or platform.machine(),
+            'cpu': cpu_name(),
             'token_agreement_with_gpu': agree, 'teacher_forced_agreement': teacher_forced,
             'teacher_forced_agree': tf_agree, 'teacher_forced_near_ties': tf_ties}
 
@@ -681,19 +712,35 @@ def main():
         torch.cuda.synchronize()
         prefill_s = time.perf_counter() - t
         eng.capture()
-        for _ in range(args.warmup):
-            eng.replay()
-        torch.cuda.synchronize()
-        e0, e1 = _events()
-        t0 = time.perf_counter()
-        e0.record()
-        for _ in range(args.steps):
-            eng.graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        gpu_s = e0.elapsed_time(e1) / 1e3
+        # Rounds of the same workload: each restores the token and position the prefill left (the cache past the
+        # prompt is rewritten by the round's own steps), replays W warm-up steps, then times K steps.
+        token0, pos0 = eng.token.clone(), eng.position.clone()
+        busy_before = gpu_busy_percent()
+        rounds = []
+        for _ in range(max(1, args.rounds)):
+            eng.token.copy_(token0)
+            eng.position.copy_(pos0)
+            for _ in range(args.warmup):
+                eng.replay()
+            torch.cuda.synchronize()
+            e0, e1 = _events()
+            t0 = time.perf_counter()
+            e0.record()
+            for _ in range(args.steps):
+                eng.graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            rounds.append((time.perf_counter() - t0, e0.elapsed_time(e1) / 1e3))
+        walls = sorted(r[0] for r in rounds)
+        wall = walls[len(walls) // 2]  # the median round (lower median for an even count)
+        gpu_s = sorted(r[1] for r in rounds)[len(rounds) // 2]
         value = args.steps / wall
+        rounds_rec = {'rounds': len(rounds), 'steps_per_round': args.steps,
+                      'tok_s': [round(args.steps / r[0], 2) for r in rounds],
+                      'median': round(value, 2), 'min': round(args.steps / walls[-1], 2),
+                      'max': round(args.steps / walls[0], 2),
+                      'gpu_busy_percent_before': busy_before,
+                      'contended': None if busy_before is None else busy_before > 10.0}
         mean_len = args.prompt + args.warmup + (args.steps + 1) / 2
 
         roof = gemv_roofline(eng)
@@ -749,6 +796,7 @@ def main():
         'metric': 'batch-1 decode tok/s (Qwen3-1.7B-shape int8); GEMV/attn HBM GB/s vs peak',
         'value': round(value, 2), 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
         'ms_per_step': round(step_s * 1e3, 4), 'gpu_ms_per_step': round(gpu_s / args.steps * 1e3, 4),
+        'spread': rounds_rec, 'host_cpu': cpu_name(),
         'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'int8',
         'data': 'synthetic: random-init weights N(0,0.02), uniform-random prompt ids',
         'config': {'workload': f'{args.model} int8 weight-only batch-1 greedy decode, {args.prompt}-token prompt, '

@@ -25,3 +25,12 @@ def test_bench_help_lists_the_contract_flags():
     assert proc.returncode == 0
     for flag in ('--gpus', '--steps', '--warmup'):
         assert flag in proc.stdout
+
+
+def test_bench_cpu_name_reads_the_model():
+    sys.path.insert(0, str(ROOT))
+    import bench
+    name = bench.cpu_name()
+    assert isinstance(name, str) and name
+    if Path('/proc/cpuinfo').exists() and 'model name' in Path('/proc/cpuinfo').read_text():
+        assert name != 'x86_64'
