@@ -117,7 +117,7 @@ class Qwen3Step(ctypes.Structure):
                 + [(name, _c_vp) for name in ('layer', 'embed', 'final_norm', 'head_w', 'head_s', 'rope_cos',
                                               'rope_sin', 'token', 'position', 'x', 'qkv', 'attn', 'act', 'logits',
                                               'workspace')]
-                + [('workspace_bytes', _c_size)])
+                + [('workspace_bytes', _c_size), ('token_ring', _c_vp), ('token_ring_slots', _c_int)])
 
 _lib = None
 
@@ -153,6 +153,23 @@ def lib():
 def check(name, status):
     if status != EGPT_OK:
         raise EgptError(name, status)
+
+
+_hip = None
+
+
+def host_device_pointer(host_ptr):
+    """The device address of pinned host memory (hipHostGetDevicePointer in the HIP runtime torch loaded), or None
+    where the runtime does not map it."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL('libamdhip64.so.7', mode=ctypes.RTLD_GLOBAL)
+        _hip.hipHostGetDevicePointer.restype = _c_int
+        _hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(_c_vp), _c_vp, ctypes.c_uint]
+    dev = _c_vp()
+    if _hip.hipHostGetDevicePointer(ctypes.byref(dev), host_ptr, 0) != 0 or not dev.value:
+        return None
+    return dev.value
 
 
 def stream_ptr(device=None):

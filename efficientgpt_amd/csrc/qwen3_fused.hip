@@ -592,17 +592,24 @@ __global__ __launch_bounds__(W * kWave) void gemv_rows_kernel(const FusedGemv a)
 }
 
 // Greedy pick over the per-block maxima: token = first index of the largest
-// logit (torch.argmax), position += 1. One block.
+// logit (torch.argmax), position += 1, and (ring set) the token also to
+// ring[new position % slots]. One block.
 __global__ __launch_bounds__(kFThreads) void argmax_final_kernel(const float* __restrict__ part_v,
                                                                  const int* __restrict__ part_i, int parts,
                                                                  int64_t* __restrict__ token,
-                                                                 int64_t* __restrict__ position) {
+                                                                 int64_t* __restrict__ position,
+                                                                 int64_t* __restrict__ ring, int slots) {
   ArgBest best{-INFINITY, 0x7fffffff};
   for (int j = threadIdx.x; j < parts; j += kFThreads) best = arg_better(best, ArgBest{part_v[j], part_i[j]});
   best = block_argbest<kFWaves>(best);
   if (threadIdx.x == 0) {
-    *token = best.i == 0x7fffffff ? 0 : best.i;  // no logits at all: token 0
-    if (position) *position += 1;
+    const int64_t tok = best.i == 0x7fffffff ? 0 : best.i;  // no logits at all: token 0
+    *token = tok;
+    if (position) {
+      const int64_t p = *position + 1;
+      *position = p;
+      if (ring) ring[(p % slots + slots) % slots] = tok;
+    }
   }
 }
 
@@ -889,6 +896,7 @@ int check_step(const egpt_qwen3_step* s) {
   }
   const StepLayout lay = step_layout(s);
   if (!s->workspace || s->workspace_bytes < lay.total || ((uintptr_t)s->workspace & 255u)) return EGPT_ERR_WORKSPACE;
+  if (s->token_ring && s->token_ring_slots < 1) return EGPT_ERR_INVALID;
   return EGPT_OK;
 }
 
@@ -1141,7 +1149,7 @@ extern "C" int egpt_argmax_parts(const float* part_v, const int* part_i, int par
                                  int64_t* position, hipStream_t stream) {
   if (!part_v || !part_i || !token || parts < 1) return EGPT_ERR_INVALID;
   hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kFThreads), 0, stream, part_v, part_i, parts, token,
-                     position);
+                     position, nullptr, 1);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -1233,6 +1241,7 @@ extern "C" int egpt_qwen3_decode_step(const egpt_qwen3_step* s, hipStream_t stre
   head_gemv(s, g);
   if ((st = run_fused(g[0], stream)) != EGPT_OK) return st;
   hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kFThreads), 0, stream, g[0].part_v, g[0].part_i,
-                     (int)head_blocks(s->vocab), s->token, s->position);
+                     (int)head_blocks(s->vocab), s->token, s->position, s->token_ring,
+                     s->token_ring ? s->token_ring_slots : 1);
   return EGPT_LAUNCH_STATUS();
 }

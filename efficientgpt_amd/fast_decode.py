@@ -3,9 +3,10 @@
 Drop-in for research/realmodel/fast_decode.py: `GraphGreedyDecoder(model,
 max_cache_len, lookahead=8)` and `.generate(input_ids, max_new_tokens, eos_ids=(),
 on_token=None) -> (tokens, stats)` keep the reference's names, guards (ValueError),
-stats keys and streaming semantics (:66-111): every step's token is copied into
-pinned host memory behind an event, a token is handed out as soon as its event has
-fired, the host never waits on the step it has just launched unless more than
+stats keys and streaming semantics (:66-111): every step's token reaches pinned
+host memory behind an event (the step's last kernel stores it to the engine's
+token ring, so no copy is launched per token), a token is handed out as soon as its
+event has fired, the host never waits on the step it has just launched unless more than
 `lookahead` steps are in flight, EOS stops the run at (and including) the EOS token,
 and tokens that steps launched ahead of it computed are never handed out.
 
@@ -98,22 +99,32 @@ class GraphGreedyDecoder:
         eng.reset()
         stop = frozenset(int(e) for e in eos_ids)
         tokens, t_first = [], None
-        in_flight = collections.deque()  # (host slot, event after its copy), oldest first
+        # (pinned host tensor, slot, event after which the slot holds the token), oldest first
+        in_flight = collections.deque()
+        # With the engine's token ring, each replay stores its token to pinned memory itself (no copy launched
+        # per token): token k of the request lands at ring slot (prompt length + k) % capacity.
+        ring = eng.token_ring if getattr(eng, '_ring_dev', None) else None
+        plen = int(input_ids.shape[1])
         t0 = time.perf_counter()
         eng.prefill(input_ids[0])  # the first new token is now in eng.token
         for step in range(max_new_tokens):
-            self.host[step:step + 1].copy_(eng.token, non_blocking=True)
-            copied = torch.cuda.Event()
-            copied.record()
-            in_flight.append((step, copied))
+            if step == 0 or ring is None:
+                self.host[step:step + 1].copy_(eng.token, non_blocking=True)
+                copied = torch.cuda.Event()
+                copied.record()
+                in_flight.append((self.host, step, copied))
             final = step + 1 == max_new_tokens
             if not final:
                 eng.graph.replay()  # overwrites eng.token with the next step's pick
+                if ring is not None:
+                    stored = torch.cuda.Event()
+                    stored.record()
+                    in_flight.append((ring, (plen + step + 1) % eng.cap, stored))
             # hand out what has landed; block only to keep the run-ahead within the lookahead, or at the end
-            while in_flight and (final or len(in_flight) > self.lookahead or in_flight[0][1].query()):
-                slot, copied = in_flight.popleft()
+            while in_flight and (final or len(in_flight) > self.lookahead or in_flight[0][2].query()):
+                buf, slot, copied = in_flight.popleft()
                 copied.synchronize()
-                tok = int(self.host[slot])
+                tok = int(buf[slot])
                 if t_first is None:
                     t_first = time.perf_counter()
                 tokens.append(tok)

@@ -236,6 +236,9 @@ class Qwen3Int8Engine:
         self.act = torch.zeros(1, c.inter, device=dev, dtype=bf)
         self.down = torch.zeros(1, c.hidden, device=dev, dtype=bf)
         self.logits = torch.zeros(1, c.vocab, device=dev, dtype=bf)
+        # every step's token, stored by the step itself at slot (new position % cap) of pinned host memory
+        self.token_ring = torch.full((cap,), -1, dtype=torch.long, pin_memory=True)
+        self._ring_dev = _lib.host_device_pointer(self.token_ring.data_ptr())
         lib = _lib.lib()
         self.nsplit = lib.egpt_qwen3_step_default_splits(c.heads, c.kv_heads, d, cap)
         need = ctypes.c_size_t()
@@ -291,6 +294,8 @@ class Qwen3Int8Engine:
         # zeroed once: the kernels' hand-off counters start at zero and are returned to zero by the kernels
         self.step_ws = torch.zeros(need.value, device=self.device, dtype=torch.uint8)
         d.workspace, d.workspace_bytes = ptr(self.step_ws), need.value
+        if self._ring_dev:
+            d.token_ring, d.token_ring_slots = self._ring_dev, self.cap
         self._step_c = d
 
     # ------------------------------------------------------------------ construction helpers

@@ -355,6 +355,13 @@ typedef struct egpt_qwen3_step {
   void *logits;
   void *workspace;
   size_t workspace_bytes;
+  /* Optional (NULL: unused): each step also stores its greedy token to
+   * token_ring[new position % token_ring_slots], where the new position is the
+   * one it leaves in *position. Pinned host memory (hipHostMalloc) lets a host
+   * loop read every step's token once that step has completed, with no copy
+   * launched per token; device memory works too. */
+  int64_t *token_ring;
+  int token_ring_slots;
 } egpt_qwen3_step;
 
 int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);

@@ -100,16 +100,18 @@ def test_struct_layouts_match_the_header(tmp_path):
     src = tmp_path / 'layout.c'
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "egpt.h"\n'
                    'int main(void) {\n'
-                   '  printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(egpt_gemv_fused), offsetof(egpt_gemv_fused, part_i),\n'
+                   '  printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(egpt_gemv_fused), offsetof(egpt_gemv_fused, part_i),\n'
                    '         offsetof(egpt_gemv_fused, w), sizeof(egpt_qwen3_step),\n'
-                   '         offsetof(egpt_qwen3_step, workspace_bytes), sizeof(egpt_qwen3_layer));\n'
+                   '         offsetof(egpt_qwen3_step, workspace_bytes), sizeof(egpt_qwen3_layer),\n'
+                   '         offsetof(egpt_qwen3_step, token_ring_slots));\n'
                    '  return 0;\n}\n')
     exe = tmp_path / 'layout'
     subprocess.run([gcc, '-D__HIP_PLATFORM_AMD__', f'-I{HEADER.parent}', '-I/opt/rocm/include', str(src), '-o', str(exe)],
                    check=True, capture_output=True)
     got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     want = [ctypes.sizeof(_lib.GemvFused), _lib.GemvFused.part_i.offset, _lib.GemvFused.w.offset,
-            ctypes.sizeof(_lib.Qwen3Step), _lib.Qwen3Step.workspace_bytes.offset, ctypes.sizeof(_lib.Qwen3Layer)]
+            ctypes.sizeof(_lib.Qwen3Step), _lib.Qwen3Step.workspace_bytes.offset, ctypes.sizeof(_lib.Qwen3Layer),
+            _lib.Qwen3Step.token_ring_slots.offset]
     assert got == want
 
 

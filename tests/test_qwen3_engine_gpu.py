@@ -312,6 +312,28 @@ def test_decoder_pool_buckets_share_weights_and_match_a_single_decoder():
         pool.generate(torch.zeros((1, 400), dtype=torch.long, device='cuda'), 200)
 
 
+def test_generate_streams_tokens_from_the_step_ring():
+    """Each graph replay stores its token to the engine's pinned token ring (slot new position % capacity), which
+    generate() reads instead of launching a copy per token; with the ring switched off the decoder copies every
+    token, and the two runs hand out the same tokens."""
+    from efficientgpt_amd.fast_decode import GraphGreedyDecoder
+    eng, _ = build(SMALL, seed=6, std=0.15, cap=96)
+    assert eng._ring_dev, 'pinned memory not mapped for the device'
+    prompt = torch.randint(0, SMALL.vocab, (1, 11), generator=torch.Generator().manual_seed(12))
+    dec = GraphGreedyDecoder(eng, max_cache_len=96, lookahead=3)
+    got, st = dec.generate(prompt.cuda(), 40)
+    assert st['tokens'] == 40
+    plen = prompt.shape[1]
+    assert [int(eng.token_ring[(plen + k) % eng.cap]) for k in range(1, 40)] == got[1:]
+    ring_dev = eng._ring_dev
+    eng._ring_dev = None  # the decoder's copy-per-token path
+    try:
+        again, _ = dec.generate(prompt.cuda(), 40)
+    finally:
+        eng._ring_dev = ring_dev
+    assert again == got
+
+
 def test_guards():
     from efficientgpt_amd.fast_decode import GraphGreedyDecoder
     eng, _ = build(TINY, seed=0, std=0.2, cap=32)
