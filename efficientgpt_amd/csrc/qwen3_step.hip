@@ -58,6 +58,63 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(uint16_t* __r
   }
 }
 
+// Element e of a row in the vector form: thread t owns 8-element groups t, t + 256, ... (16-byte accesses).
+// The same arithmetic per element as add_rmsnorm_kernel; the sum of squares runs in this element order.
+__device__ __forceinline__ void unpack8(const u32x4 v, float (&f)[8]) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(u[i]);
+    f[2 * i + 1] = bf16_hi(u[i]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  uint32_t u[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) u[i] = (uint32_t)f32_to_bf16(f[2 * i]) | ((uint32_t)f32_to_bf16(f[2 * i + 1]) << 16);
+  return u32x4{u[0], u[1], u[2], u[3]};
+}
+
+// add_rmsnorm_kernel for rows of a multiple of 8 elements, 16-byte aligned: every access 16 bytes wide (the
+// scalar form issues one 2-byte access per element and per thread, 0.25-0.3 of HBM peak at 8192 rows).
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_v8_kernel(uint16_t* __restrict__ x, int64_t ldx,
+                                                                      const uint16_t* __restrict__ a, int64_t lda,
+                                                                      const uint16_t* __restrict__ w,
+                                                                      uint16_t* __restrict__ y, int64_t ldy, int n,
+                                                                      float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  extern __shared__ float rowbuf[];  // n floats: the (updated) residual row
+  const int64_t row = blockIdx.x;
+  uint16_t* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int g = threadIdx.x; g * 8 < n; g += kNormThreads) {
+    float v[8];
+    unpack8(ld16(xr + g * 8), v);
+    if (a) {
+      float av[8];
+      unpack8(ld16(a + row * lda + g * 8), av);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = bf16r(v[e] + av[e]);
+      *(u32x4*)(xr + g * 8) = pack8(v);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      rowbuf[g * 8 + e] = v[e];
+      ss = fmaf(v[e], v[e], ss);
+    }
+  }
+  const float total = block_sum_256(ss, red);
+  const float inv = rsqrtf(total / (float)n + eps);
+  uint16_t* yr = y + row * ldy;
+  for (int g = threadIdx.x; g * 8 < n; g += kNormThreads) {
+    float wv[8], o[8];
+    unpack8(ld16(w + g * 8), wv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = wv[e] * bf16r(rowbuf[g * 8 + e] * inv);
+    *(u32x4*)(yr + g * 8) = pack8(o);
+  }
+}
+
 // q/k RMSNorm + RoPE + cache write. One wavefront per (row, head); heads
 // 0..Hq-1 are query heads (written to q_out), Hq..Hq+Hkv-1 key heads (normed,
 // rotated, written to the key cache at the row's position), the last Hkv value
@@ -141,6 +198,24 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   out[row * ld_out + c] = f32_to_bf16(sg * u);
 }
 
+// silu_mul_kernel with 8 elements per thread and 16-byte accesses, block (column chunk, row): for inter, the
+// row strides and the pointers multiples of 8 elements / 16 bytes. The same arithmetic per element.
+__global__ __launch_bounds__(256) void silu_mul_v8_kernel(const uint16_t* __restrict__ gu, int64_t ld_gu, int inter,
+                                                          uint16_t* __restrict__ out, int64_t ld_out) {
+  const int64_t row = blockIdx.y;
+  const int c = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 8;
+  if (c >= inter) return;
+  float g[8], u[8], o[8];
+  unpack8(ld16(gu + row * ld_gu + c), g);
+  unpack8(ld16(gu + row * ld_gu + inter + c), u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float sg = bf16r(g[e] / (1.0f + expf(-g[e])));
+    o[e] = sg * u[e];
+  }
+  *(u32x4*)(out + row * ld_out + c) = pack8(o);
+}
+
 // Embedding gather: out[r, :] = table[token[r], :].
 __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ tokens, const uint16_t* __restrict__ table,
                                                     int64_t ld_table, int vocab, uint16_t* __restrict__ out,
@@ -215,7 +290,7 @@ constexpr int kArgParts = 256;
 
 // launch_reduce_add_rmsnorm's kernel: S split partials per element, every load of an element issued before its
 // first addition (the reduce kernel's order: v0 + v1 + ... + v(S-1)).
-template <int S>
+template <int S, bool V8>
 __global__ __launch_bounds__(kNormThreads) void reduce_add_rmsnorm_kernel(const float* __restrict__ part,
                                                                          const float* __restrict__ scale,
                                                                          uint16_t* __restrict__ x, int64_t ldx,
@@ -229,26 +304,68 @@ __global__ __launch_bounds__(kNormThreads) void reduce_add_rmsnorm_kernel(const 
   const float* pr = part + row * n;
   uint16_t* xr = x + row * ldx;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < n; i += kNormThreads) {
-    float v[S];
+  if (V8) {  // add_rmsnorm_v8_kernel's element order (8-element groups per thread)
+    for (int g = threadIdx.x; g * 8 < n; g += kNormThreads) {
+      float xv[8], r[8];
+      unpack8(ld16(xr + g * 8), xv);
 #pragma unroll
-    for (int sp = 0; sp < S; ++sp) v[sp] = pr[sp * mn + i];
-    float acc = v[0];
+      for (int e = 0; e < 8; ++e) {
+        const int i = g * 8 + e;
+        float v[S];
 #pragma unroll
-    for (int sp = 1; sp < S; ++sp) acc += v[sp];
-    const float o = bf16r(bf16r(acc) * scale[i]);  // the GEMM's output element, as the reduce kernel rounds it
-    const float r = bf16r(bf16_to_f32(xr[i]) + o);
-    xr[i] = f32_to_bf16(r);
-    rowbuf[i] = r;
-    ss = fmaf(r, r, ss);
+        for (int sp = 0; sp < S; ++sp) v[sp] = pr[sp * mn + i];
+        float acc = v[0];
+#pragma unroll
+        for (int sp = 1; sp < S; ++sp) acc += v[sp];
+        const float o = bf16r(bf16r(acc) * scale[i]);
+        r[e] = bf16r(xv[e] + o);
+        rowbuf[i] = r[e];
+        ss = fmaf(r[e], r[e], ss);
+      }
+      *(u32x4*)(xr + g * 8) = pack8(r);
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += kNormThreads) {
+      float v[S];
+#pragma unroll
+      for (int sp = 0; sp < S; ++sp) v[sp] = pr[sp * mn + i];
+      float acc = v[0];
+#pragma unroll
+      for (int sp = 1; sp < S; ++sp) acc += v[sp];
+      const float o = bf16r(bf16r(acc) * scale[i]);  // the GEMM's output element, as the reduce kernel rounds it
+      const float r = bf16r(bf16_to_f32(xr[i]) + o);
+      xr[i] = f32_to_bf16(r);
+      rowbuf[i] = r;
+      ss = fmaf(r, r, ss);
+    }
   }
   const float total = block_sum_256(ss, red);
   const float inv = rsqrtf(total / (float)n + eps);
   uint16_t* yr = y + row * ldy;
-  for (int i = threadIdx.x; i < n; i += kNormThreads) yr[i] = f32_to_bf16(bf16_to_f32(w[i]) * bf16r(rowbuf[i] * inv));
+  if (V8) {
+    for (int g = threadIdx.x; g * 8 < n; g += kNormThreads) {
+      float wv[8], o[8];
+      unpack8(ld16(w + g * 8), wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = wv[e] * bf16r(rowbuf[g * 8 + e] * inv);
+      *(u32x4*)(yr + g * 8) = pack8(o);
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += kNormThreads)
+      yr[i] = f32_to_bf16(bf16_to_f32(w[i]) * bf16r(rowbuf[i] * inv));
+  }
 }
 
 constexpr int kReduceNormMaxSplits = 16;
+
+bool aligned16p(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Whether a norm's rows take the vector form: whole 8-element groups, 16-byte aligned rows.
+bool v8_row(const void* x, int64_t ldx, const void* w, const void* y, int64_t ldy, int n, const void* a = nullptr,
+            int64_t lda = 0) {
+  return n % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && lda % 8 == 0 && aligned16p(x) && aligned16p(w) &&
+         aligned16p(y) && aligned16p(a);
+}
 
 template <int S>
 int launch_reduce_norm(int splits, dim3 grid, size_t lds, hipStream_t st, const float* part, const float* scale,
@@ -259,8 +376,12 @@ int launch_reduce_norm(int splits, dim3 grid, size_t lds, hipStream_t st, const 
   } else {
     if (splits != S)
       return launch_reduce_norm<S - 1>(splits, grid, lds, st, part, scale, x, ldx, w, y, ldy, M, n, eps);
-    hipLaunchKernelGGL(reduce_add_rmsnorm_kernel<S>, grid, dim3(kNormThreads), lds, st, part, scale, x, ldx, w, y,
-                       ldy, M, n, eps);
+    if (v8_row(x, ldx, w, y, ldy, n))
+      hipLaunchKernelGGL((reduce_add_rmsnorm_kernel<S, true>), grid, dim3(kNormThreads), lds, st, part, scale, x, ldx,
+                         w, y, ldy, M, n, eps);
+    else
+      hipLaunchKernelGGL((reduce_add_rmsnorm_kernel<S, false>), grid, dim3(kNormThreads), lds, st, part, scale, x,
+                         ldx, w, y, ldy, M, n, eps);
     return EGPT_LAUNCH_STATUS();
   }
 }
@@ -287,8 +408,9 @@ extern "C" int egpt_rmsnorm(const void* x, int64_t ldx, const void* w, void* y, 
   if (!x || !w || !y || rows < 0 || n < 1 || ldx < n || ldy < n) return EGPT_ERR_INVALID;
   if ((size_t)n * sizeof(float) > 64 * 1024) return EGPT_ERR_UNSUPPORTED;
   if (rows == 0) return EGPT_OK;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), n * sizeof(float), stream, (uint16_t*)x, ldx,
-                     (const uint16_t*)nullptr, 0, (const uint16_t*)w, (uint16_t*)y, ldy, n, eps);
+  hipLaunchKernelGGL(v8_row(x, ldx, w, y, ldy, n) ? add_rmsnorm_v8_kernel : add_rmsnorm_kernel, dim3(rows),
+                     dim3(kNormThreads), n * sizeof(float), stream, (uint16_t*)x, ldx, (const uint16_t*)nullptr, 0,
+                     (const uint16_t*)w, (uint16_t*)y, ldy, n, eps);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -297,8 +419,9 @@ extern "C" int egpt_add_rmsnorm(void* x, int64_t ldx, const void* a, int64_t lda
   if (!x || !a || !w || !y || rows < 0 || n < 1 || ldx < n || lda < n || ldy < n) return EGPT_ERR_INVALID;
   if ((size_t)n * sizeof(float) > 64 * 1024) return EGPT_ERR_UNSUPPORTED;
   if (rows == 0) return EGPT_OK;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kNormThreads), n * sizeof(float), stream, (uint16_t*)x, ldx,
-                     (const uint16_t*)a, lda, (const uint16_t*)w, (uint16_t*)y, ldy, n, eps);
+  hipLaunchKernelGGL(v8_row(x, ldx, w, y, ldy, n, a, lda) ? add_rmsnorm_v8_kernel : add_rmsnorm_kernel, dim3(rows),
+                     dim3(kNormThreads), n * sizeof(float), stream, (uint16_t*)x, ldx, (const uint16_t*)a, lda,
+                     (const uint16_t*)w, (uint16_t*)y, ldy, n, eps);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -338,6 +461,11 @@ extern "C" int egpt_silu_mul(const void* gu, int64_t ld_gu, int inter, void* out
                              hipStream_t stream) {
   if (!gu || !out || inter < 1 || rows < 0 || ld_gu < 2 * (int64_t)inter || ld_out < inter) return EGPT_ERR_INVALID;
   if (rows == 0) return EGPT_OK;
+  if (inter % 8 == 0 && ld_gu % 8 == 0 && ld_out % 8 == 0 && aligned16p(gu) && aligned16p(out) && rows <= 65535) {
+    hipLaunchKernelGGL(silu_mul_v8_kernel, dim3((unsigned)((inter / 8 + 255) / 256), (unsigned)rows), dim3(256), 0,
+                       stream, (const uint16_t*)gu, ld_gu, inter, (uint16_t*)out, ld_out);
+    return EGPT_LAUNCH_STATUS();
+  }
   const int64_t total = (int64_t)rows * inter;
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
                      (const uint16_t*)gu, ld_gu, inter, (uint16_t*)out, ld_out, rows);
