@@ -186,6 +186,46 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 }
 
 // act = bf16( bf16(silu(gate)) * up ), gate/up interleaved per row as [gate(inter) | up(inter)].
+// qk_norm_rope_kernel for 16-byte aligned rows: a (row, head) job per group of D / 8 lanes, 8 elements per lane
+// and 16-byte accesses (the wavefront-per-head form issues 2-byte accesses). Query and key heads take the decode
+// step's head_norm_rope (the same per-element roundings and the same lane layout and sum order as the step's
+// attention kernel), value heads a 16-byte copy. Groups past the last job compute the last one and store nothing.
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_v8_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld_qkv, const int64_t* __restrict__ positions,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, uint16_t* __restrict__ q_out, int64_t ld_q, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int64_t c_sh, int64_t c_sn, int rows, int Hq, int Hkv, int cap, float eps) {
+  constexpr int EPL = 8;
+  constexpr int LPS = D / EPL;  // lanes per head: 16 at D 128
+  const int heads = Hq + 2 * Hkv;
+  const int64_t jobs = (int64_t)rows * heads;
+  const int64_t job_raw = (int64_t)blockIdx.x * (256 / LPS) + threadIdx.x / LPS;
+  const bool store = job_raw < jobs;
+  const int64_t job = store ? job_raw : jobs - 1;
+  const int64_t row = job / heads;
+  const int head = (int)(job % heads);
+  const int d0 = (threadIdx.x % LPS) * EPL;
+  int64_t pos = positions[row];
+  pos = pos < 0 ? 0 : (pos >= cap ? cap - 1 : pos);
+  const u32x4 xr = ld16(qkv + row * ld_qkv + (int64_t)head * D + d0);
+  if (head >= Hq + Hkv) {  // value head: straight copy into the cache (group-uniform)
+    if (store) *(u32x4*)(v_cache + (int64_t)(head - Hq - Hkv) * c_sh + pos * c_sn + d0) = xr;
+    return;
+  }
+  const bool is_q = head < Hq;
+  const u32x4 wr = ld16((is_q ? qn_w : kn_w) + d0);
+  const u32x4 cr = ld16(cos_t + pos * D + d0);
+  const u32x4 sr = ld16(sin_t + pos * D + d0);
+  float o[EPL];
+  head_norm_rope<D, EPL, LPS>(xr, wr, cr, sr, d0, eps, o);
+  uint32_t pk[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pk[e] = (uint32_t)f32_to_bf16(o[2 * e]) | ((uint32_t)f32_to_bf16(o[2 * e + 1]) << 16);
+  uint16_t* dst = is_q ? q_out + row * ld_q + (int64_t)head * D : k_cache + (int64_t)(head - Hq) * c_sh + pos * c_sn;
+  if (store) *(u32x4*)(dst + d0) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t ld_gu, int inter,
                                                        uint16_t* __restrict__ out, int64_t ld_out, int rows) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -435,6 +475,23 @@ extern "C" int egpt_qk_norm_rope(const void* qkv, int64_t ld_qkv, const int64_t*
     return EGPT_ERR_INVALID;
   if (rows == 0) return EGPT_OK;
   const int64_t jobs = (int64_t)rows * (Hq + 2 * Hkv);
+  const bool v8 = ld_qkv % 8 == 0 && ld_q % 8 == 0 && cache_head_stride % 8 == 0 && cache_slot_stride % 8 == 0 &&
+                  aligned16p(qkv) && aligned16p(q_out) && aligned16p(k_cache) && aligned16p(v_cache) &&
+                  aligned16p(q_norm_w) && aligned16p(k_norm_w) && aligned16p(cos_t) && aligned16p(sin_t);
+  if (v8 && (D == 128 || D == 64 || D == 32)) {
+    const int per_block = 256 / (D / 8);  // (row, head) jobs per block
+    const dim3 g8((unsigned)((jobs + per_block - 1) / per_block));
+#define EGPT_QKV8(DD)                                                                                                \
+  hipLaunchKernelGGL((qk_norm_rope_v8_kernel<DD>), g8, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, positions, \
+                     (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,                    \
+                     (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,          \
+                     cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps)
+    if (D == 128) EGPT_QKV8(128);
+    else if (D == 64) EGPT_QKV8(64);
+    else EGPT_QKV8(32);
+#undef EGPT_QKV8
+    return EGPT_LAUNCH_STATUS();
+  }
   dim3 grid((unsigned)((jobs + 3) / 4));
   if (D == 128) {
     hipLaunchKernelGGL((qk_norm_rope_kernel<128>), grid, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, positions,

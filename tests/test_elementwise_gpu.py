@@ -85,3 +85,67 @@ def test_add_rmsnorm_vector_and_scalar_forms_agree(rows, n):
     dvs = np.abs(yv.double().cpu().numpy() - ys[:, 1:].double().cpu().numpy())
     assert np.all(dvs <= 2 * _ulp(want)) and np.mean(dvs == 0) >= 0.99
     assert torch.equal(yv, yn)  # the same vector kernel over the same rows
+
+
+@pytest.mark.parametrize('d,hq,hkv,rows', [(128, 32, 8, 4096), (128, 16, 8, 100), (64, 6, 6, 33), (32, 4, 2, 17)])
+def test_qk_norm_rope_vector_and_scalar_forms_agree(d, hq, hkv, rows):
+    """egpt_qk_norm_rope over a prompt block: query heads normalised and rotated into q_out, key heads into the key
+    cache at each row's position, value heads copied into the value cache. The vector form (16-byte rows) against
+    the wavefront-per-head form (rows one element off alignment): value copies bit-identical, normalised heads to
+    two bf16 ulps of the larger RoPE term (the head's mean of squares in another fp32 order) and 99% bit-identical;
+    both within three such ulps of an fp64 restatement of transformers' q/k norm and RoPE (modeling_qwen3.py:
+    139-166, 237-256)."""
+    lib = _lib.lib()
+    g = torch.Generator().manual_seed(d + hq + rows)
+    cap, pos0 = rows + 40, 25
+    n = (hq + 2 * hkv) * d
+    qkv = torch.randn(rows, n, generator=g).to(torch.bfloat16)
+    qn = (1 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kn = (1 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float) / d))
+    ang = torch.arange(cap, dtype=torch.float)[:, None] * inv_freq[None, :]
+    emb = torch.cat([ang, ang], 1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    positions = torch.arange(pos0, pos0 + rows, dtype=torch.long)
+    st = _lib.stream_ptr()
+
+    def run(offset):
+        src = torch.zeros(rows, n + offset, dtype=torch.bfloat16, device='cuda')
+        src[:, offset:] = qkv.cuda()
+        q = torch.zeros(rows, hq * d + offset, dtype=torch.bfloat16, device='cuda')
+        kc = torch.zeros(hkv, cap, d, dtype=torch.bfloat16, device='cuda')
+        vc = torch.zeros_like(kc)
+        assert lib.egpt_qk_norm_rope(src[:, offset:].data_ptr(), n + offset, positions.cuda().data_ptr(),
+                                     qn.cuda().data_ptr(), kn.cuda().data_ptr(), cos.cuda().data_ptr(),
+                                     sin.cuda().data_ptr(), q[:, offset:].data_ptr(), hq * d + offset, kc.data_ptr(),
+                                     vc.data_ptr(), kc.stride(0), kc.stride(1), rows, hq, hkv, d, cap, 1e-6, st) == 0
+        torch.cuda.synchronize()
+        return q[:, offset:].cpu(), kc.cpu(), vc.cpu()
+
+    qv, kv, vv = run(0)
+    qs, ks, vs = run(1)
+    assert torch.equal(vv, vs)
+    assert torch.equal(vv[:, pos0:pos0 + rows], qkv[:, (hq + hkv) * d:].view(rows, hkv, d).transpose(0, 1))
+
+    def truth(x, w):  # x [rows, heads, d] bf16 -> (the roundings in fp64, the larger of the two RoPE terms)
+        xf = x.double()
+        normed = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16).double()
+        normed = (w.double() * normed).to(torch.bfloat16).double()
+        rot = torch.cat([-normed[..., d // 2:], normed[..., :d // 2]], -1)
+        c, s = cos[positions].double()[:, None], sin[positions].double()[:, None]
+        a, b = (normed * c).to(torch.bfloat16).double(), (rot * s).to(torch.bfloat16).double()
+        return (a + b).to(torch.bfloat16), torch.maximum(a.abs(), b.abs())
+
+    want_q, mag_q = truth(qkv[:, :hq * d].view(rows, hq, d), qn)
+    want_k, mag_k = truth(qkv[:, hq * d:(hq + hkv) * d].view(rows, hkv, d), kn)
+    cases = ((qv, qs, want_q.view(rows, hq * d), mag_q.view(rows, hq * d)),
+             (kv[:, pos0:pos0 + rows], ks[:, pos0:pos0 + rows], want_k.transpose(0, 1), mag_k.transpose(0, 1)))
+    for got, other, want, mag in cases:
+        # a flipped rounding of a normalised element moves each RoPE term by up to an ulp of that term: near a
+        # cancelling sum that is many ulps of the result, so the bound is in ulps of the larger term
+        w64, unit = want.double().numpy(), _ulp(np.maximum(np.abs(want.double().numpy()), mag.numpy()))
+        for y in (got, other):
+            dd = np.abs(y.double().numpy() - w64)
+            assert np.all(dd <= 3 * unit), float((dd / unit).max())
+        dvs = np.abs(got.double().numpy() - other.double().numpy())
+        assert np.all(dvs <= 2 * unit) and np.mean(dvs == 0) >= 0.99
