@@ -35,6 +35,8 @@ SIGNATURES = {
     'egpt_int8_gemm_workspace': (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
     'egpt_int8_gemm_ws': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
                                    _c_vp, _c_size, _c_vp]),
+    'egpt_int8_gemm_swiglu': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
+                                       _c_vp]),
     'egpt_int8_gemm_add_rmsnorm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64,
                                             _c_int, _c_int, _c_int, ctypes.c_float, _c_vp, _c_size, _c_vp]),
     'egpt_int8_gemv_splitk_workspace': (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),

@@ -85,7 +85,19 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int splits, kchunk;  // K slices (1: no split) of kchunk columns each, the last one shorter
   float* part;         // splits > 1: fp32 partial tiles [splits][M][N]
+  int inter;           // SwiGLU form: features (w holds inter gate rows, then inter up rows; N = 2 inter)
 };
+
+// SwiGLU form: block tile column j (of BN) -> weight row. Each wavefront's BN / WN columns hold half of its
+// features' gate rows and then the same features' up rows, so gate and up of a feature land in the same lane
+// and accumulator register of a wavefront's tiles tn and tn + TN / 2. Features past `inter` read the last one.
+template <int BN, int WN>
+__device__ __forceinline__ int64_t swiglu_row(int64_t pid_n, int j, int inter) {
+  constexpr int kPerWave = BN / WN, kHalf = kPerWave / 2;
+  const int wn = j / kPerWave, o = j % kPerWave;
+  const int64_t f = min(pid_n * (BN / 2) + wn * kHalf + (o % kHalf), (int64_t)inter - 1);
+  return o < kHalf ? f : inter + f;
+}
 
 // Wavefronts of the 128 x 256 and 128 x 128 tiles, and how many of them lie along N.
 constexpr int kNW256 = 4;
@@ -123,10 +135,11 @@ __device__ __forceinline__ void gemm_tile(int b, int tiles_m, int tiles_n, int& 
   pid_n = (t % group) / gm;
 }
 
-template <int BM, int BN, int BK, bool SPLIT, int WN, int NW>
+template <int BM, int BN, int BK, bool SPLIT, int WN, int NW, bool SWIGLU = false>
 __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8_gemm_kernel(const GemmArgs a) {
   using S = GemmShape<BM, BN, BK, WN, NW>;
   constexpr int TM = S::TM, TN = S::TN;
+  static_assert(!SWIGLU || (!SPLIT && TN % 2 == 0), "the SwiGLU form pairs a wavefront's column tiles");
   constexpr int kLdsRow = S::kLdsRow, kLdsRowW = S::kLdsRowW;
   __shared__ __align__(16) uint16_t As[2][BM * kLdsRow];
   __shared__ __align__(16) int8_t Bs[2][BN * kLdsRowW];
@@ -163,7 +176,8 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
   for (int j = 0; j < S::kBLoads; ++j) {
     const int i = tid + j * S::NT;
     const int row = i / (BK / 16), chunk = i % (BK / 16);
-    woff[j] = (uint32_t)(min(n0 + row, (int64_t)a.N - 1) * a.ldw + kbeg + chunk * 16);
+    const int64_t wrow = SWIGLU ? swiglu_row<BN, WN>(pid_n, row, a.inter) : min(n0 + row, (int64_t)a.N - 1);
+    woff[j] = (uint32_t)(wrow * a.ldw + kbeg + chunk * 16);
     b_lds[j] = row * kLdsRowW + chunk * 16;
   }
   // Two register staging sets: the loads of step k + 2 are issued while step k is
@@ -300,6 +314,32 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
   char* yb = (char*)a.y;
   const int64_t mrow0 = m0 + wm0 + 4 * (lane / 32);
   const uint32_t pitch = (uint32_t)(a.ldy * 2);
+  if constexpr (SWIGLU) {
+    // act = bf16(bf16(silu(g)) * u) with g and u the product's two roundings (the reference's prefill formula
+    // for each), SwiGLU rounded as transformers' bf16 Qwen3MLP (models/qwen3/modeling_qwen3.py:49-62): the same
+    // arithmetic per element as the GEMM followed by egpt_silu_mul.
+#pragma unroll
+    for (int tn = 0; tn < TN / 2; ++tn) {
+      const int64_t f = (int64_t)pid_n * (BN / 2) + (wave % WN) * (BN / WN / 2) + tn * 32 + lane % 32;
+      const int64_t fc = min(f, (int64_t)a.inter - 1);
+      const float sg_scale = a.scale[fc], su_scale = a.scale[a.inter + fc];
+      const uint32_t base = (uint32_t)((mrow0 * a.ldy + f) * 2);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dm = tm * 32 + 8 * (r / 4) + r % 4;
+          if (mrow0 + dm < a.M && f < a.inter) {
+            const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][tn][r])) * sg_scale));
+            const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][tn + TN / 2][r])) * su_scale));
+            const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
+            *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(sg * u);
+          }
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     const int64_t n = n0 + wn0 + tn * 32 + lane % 32;
@@ -497,6 +537,40 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
   if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128, kWN128, kNW128>(a, stream);
   if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
   return launch_gemm<64, 64>(a, stream);
+}
+
+extern "C" int egpt_int8_gemm_swiglu(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale,
+                                     void* act, int64_t ld_act, int M, int inter, int K, hipStream_t stream) {
+  if (!x || !w || !scale || !act || M < 0 || inter < 0 || K < 0) return EGPT_ERR_INVALID;
+  if (ldx < K || ldw < K || ld_act < inter) return EGPT_ERR_INVALID;
+  if (M == 0 || inter == 0) return EGPT_OK;
+  const int64_t N = 2 * (int64_t)inter;
+  if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16 ||
+      (int64_t)M * ldx * 2 >= ((int64_t)1 << 31) || N * ldw >= ((int64_t)1 << 31) ||
+      (int64_t)M * ld_act * 2 >= ((int64_t)1 << 31) || N > INT32_MAX)
+    return EGPT_ERR_UNSUPPORTED;
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)act, ld_act, M, (int)N, K, 0, 0, 1, K, nullptr,
+             inter};
+  // The tiles whose wavefronts own two column tiles (a feature's gate and up in one lane), where the plain
+  // product would take them: 256 x 256 and 128 x 256 (each block covers BN / 2 features).
+  auto blocks = [&](int bm, int bn) {
+    return (int64_t)((M + bm - 1) / bm) * ((inter + bn / 2 - 1) / (bn / 2));
+  };
+  if (M > 128 && blocks(256, 256) >= 256) {
+    a.tiles_m = (M + 255) / 256;
+    a.tiles_n = (inter + 127) / 128;
+    hipLaunchKernelGGL((int8_gemm_kernel<256, 256, kBK, false, kWN256x256, kNW256x256, true>),
+                       dim3((unsigned)(a.tiles_m * a.tiles_n)), dim3(kNW256x256 * kWave), 0, stream, a);
+    return EGPT_LAUNCH_STATUS();
+  }
+  if (M > 64 && blocks(128, 256) >= 256) {
+    a.tiles_m = (M + 127) / 128;
+    a.tiles_n = (inter + 127) / 128;
+    hipLaunchKernelGGL((int8_gemm_kernel<128, 256, kBK, false, kWN256, kNW256, true>),
+                       dim3((unsigned)(a.tiles_m * a.tiles_n)), dim3(kNW256 * kWave), 0, stream, a);
+    return EGPT_LAUNCH_STATUS();
+  }
+  return EGPT_ERR_UNSUPPORTED;
 }
 
 extern "C" int egpt_int8_gemm_add_rmsnorm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw,

@@ -199,8 +199,9 @@ class Qwen3Int8Engine:
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
 
         # Prompt passes fold the residual add + RMSNorm after o_proj and down_proj into the split-K GEMM's reduce
-        # (egpt_int8_gemm_add_rmsnorm) and the next layer's input norm into the down projection; False runs the
-        # separate linear and egpt_add_rmsnorm calls instead (the same bits).
+        # (egpt_int8_gemm_add_rmsnorm), the next layer's input norm into the down projection and SwiGLU into the
+        # gate/up GEMM (egpt_int8_gemm_swiglu); False runs the separate linear, egpt_add_rmsnorm and egpt_silu_mul
+        # calls instead (the same bits).
         self.fold_norms = True
         pk = weights if packed else pack_qwen3(c, weights)
         check_packed(c, pk)
@@ -452,9 +453,17 @@ class Qwen3Int8Engine:
         else:
             self._kernel_attention(qrot, kc, vc, rows, positions, pos_stride, attn)
         self._linear_add_norm(attn, L['o_q'], L['o_s'], o, x, L['post_w'], h, rows, ws)
-        self._linear(h, L['gu_q'], L['gu_s'], gu, rows, ws)
-        _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
-                                                      act.stride(0), rows, st))
+        fused = _lib.EGPT_ERR_UNSUPPORTED
+        if rows > MAX_DECODE_ROWS and self.fold_norms:  # SwiGLU in the gate/up GEMM's epilogue
+            fused = lib.egpt_int8_gemm_swiglu(h.data_ptr(), h.stride(0), L['gu_q'].data_ptr(), L['gu_q'].stride(0),
+                                              L['gu_s'].data_ptr(), act.data_ptr(), act.stride(0), rows, c.inter,
+                                              c.hidden, st)
+        if fused == _lib.EGPT_ERR_UNSUPPORTED:
+            self._linear(h, L['gu_q'], L['gu_s'], gu, rows, ws)
+            _lib.check('egpt_silu_mul', lib.egpt_silu_mul(gu.data_ptr(), gu.stride(0), c.inter, act.data_ptr(),
+                                                          act.stride(0), rows, st))
+        else:
+            _lib.check('egpt_int8_gemm_swiglu', fused)
         if i + 1 < c.layers and rows > MAX_DECODE_ROWS and self.fold_norms:
             # the next layer's input norm folds into this projection
             self._linear_add_norm(act, L['down_q'], L['down_s'], down, x, self.layers[i + 1]['in_w'], h, rows, ws)

@@ -103,6 +103,17 @@ int egpt_int8_gemm_workspace(int M, int N, int K, size_t *bytes);
 int egpt_int8_gemm_ws(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                       void *y, int64_t ldy, int M, int N, int K, void *workspace, size_t workspace_bytes,
                       hipStream_t stream);
+/* The product of a gate/up weight pair followed by SwiGLU: w holds `inter` gate rows then `inter` up rows
+ * (int8 [2 inter, K], scales fp32 [2 inter]); for each row m and feature f, g and u are the product's values of
+ * rows f and inter + f (the two roundings above) and act[m, f] = bf16(bf16(silu(g)) * u), transformers' bf16
+ * Qwen3MLP rounding (models/qwen3/modeling_qwen3.py:49-62). The same bits as egpt_int8_gemm into a
+ * [M, 2 inter] buffer followed by egpt_silu_mul, without that buffer. Only for M > 64 rows and shapes whose large
+ * tiles fill the chip (K a multiple of 64, aligned rows, operands under 2 GiB); EGPT_ERR_UNSUPPORTED otherwise,
+ * before any launch (the caller runs the two calls). Replaces, with the product, the reference's prefill formula
+ * for gate_proj / up_proj (research/realmodel/int8_linear.py:96-97) and the SwiGLU its Inductor graph fuses
+ * after them. */
+int egpt_int8_gemm_swiglu(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                          void *act, int64_t ld_act, int M, int inter, int K, hipStream_t stream);
 /* The split-K product followed by the residual update and RMSNorm of each output row, the pair that follows
  * o_proj and down_proj in a prompt pass (transformers' Qwen3 decoder layer, models/qwen3/modeling_qwen3.py:285-322:
  * residual add, then the next RMSNorm): o = the product above, resid = bf16(resid + o) (written back), y =

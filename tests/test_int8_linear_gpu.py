@@ -402,3 +402,27 @@ def test_gemm_add_rmsnorm_matches_the_two_calls_bit_for_bit(m, k, n):
     assert lib.egpt_int8_gemm_add_rmsnorm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), r1.data_ptr(), n,
                                           nw.data_ptr(), h1.data_ptr(), n, 1024, n, k, 1e-6, ws.data_ptr(),
                                           need.value, st) == _lib.EGPT_ERR_UNSUPPORTED  # 1024 rows: K not split
+
+
+@pytest.mark.parametrize('m,k,inter', [(1024, 2048, 6144), (2048, 4096, 12288), (1100, 512, 7000)])
+def test_gemm_swiglu_matches_the_two_calls_bit_for_bit(m, k, inter):
+    """egpt_int8_gemm_swiglu (SwiGLU in the epilogue of the gate/up product, the gate and up rows of a feature
+    paired in one wavefront) against egpt_int8_gemm into a [m, 2 inter] buffer followed by egpt_silu_mul: the same
+    bits, ragged rows and features included; shapes whose large tiles would not fill the chip are refused."""
+    from efficientgpt_amd import _lib
+    lib = _lib.lib()
+    x, q, s = make_case(m, k, 2 * inter, seed=m + inter)
+    xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
+    st = _lib.stream_ptr()
+    gu = torch.empty(m, 2 * inter, device='cuda', dtype=torch.bfloat16)
+    assert lib.egpt_int8_gemm(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), gu.data_ptr(), 2 * inter, m,
+                              2 * inter, k, st) == 0
+    two = torch.empty(m, inter, device='cuda', dtype=torch.bfloat16)
+    assert lib.egpt_silu_mul(gu.data_ptr(), 2 * inter, inter, two.data_ptr(), inter, m, st) == 0
+    one = torch.full((m, inter), float('nan'), device='cuda', dtype=torch.bfloat16)
+    assert lib.egpt_int8_gemm_swiglu(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), one.data_ptr(), inter, m,
+                                     inter, k, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(one, two)
+    assert lib.egpt_int8_gemm_swiglu(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), one.data_ptr(), inter, 100,
+                                     inter, k, st) == _lib.EGPT_ERR_UNSUPPORTED  # 100 rows: the tiles do not fill

@@ -141,14 +141,15 @@ def test_fused_step_matches_unfused_step(shape, std, cap, plen):
 
 
 @pytest.mark.parametrize('shape', [SMALL, SMALL8])
-@pytest.mark.parametrize('plen', [40, 128])
+@pytest.mark.parametrize('plen', [40, 128, 4096])
 def test_prefill_folded_norms_equal_separate_calls(shape, plen):
     """Prompts of 17-128 rows take the split-K GEMM for o_proj and down_proj, with the residual add + RMSNorm folded
     into its reduce (egpt_int8_gemm_add_rmsnorm) and each down projection also taking the next layer's input norm
-    (the first layer normalises its embedding rows itself; the last leaves x + down to the head). The same prompt
-    with the folds turned off (separate linear and egpt_add_rmsnorm calls, each layer normalising its own input)
-    must give the same logits and the same K/V caches, bit for bit."""
-    eng, _ = build(shape, seed=9, std=0.15, cap=160)
+    (the first layer normalises its embedding rows itself; the last leaves x + down to the head); a 4096-row prompt
+    takes SwiGLU in the gate/up GEMM's epilogue (egpt_int8_gemm_swiglu). The same prompt with the folds turned off
+    (separate linear, egpt_add_rmsnorm and egpt_silu_mul calls, each layer normalising its own input) must give the
+    same logits and the same K/V caches, bit for bit."""
+    eng, _ = build(shape, seed=9, std=0.15, cap=max(160, plen + 8))
     prompt = torch.randint(0, shape.vocab, (plen,), generator=torch.Generator().manual_seed(plen))
     out = []
     for fold in (True, False):
