@@ -251,7 +251,8 @@ def test_qwen3_8b_full_model_8192_prompt_fused_matches_unfused(qwen3_8b_long):
     Over 36 layers the two forms' different attention summation orders move the logits by several bf16 ulps, so
     the bound is measured in the same run: the one-kernel-per-op step with its attention split 24 ways instead of
     32 (the same arithmetic in another order). The fused step may differ from the unfused one by at most twice
-    that (and always passes within 2e-2 of the largest logit); K/V likewise."""
+    that (and always passes within 2e-2 of the largest logit); K/V likewise. A pick may differ only at a near-tie
+    of the unfused logits."""
     eng = qwen3_8b_long
     assert eng.nsplit > 24, eng.nsplit  # the separate merge launch
     prompt = _qwen3_8b_long_prompt()
@@ -288,7 +289,14 @@ def test_qwen3_8b_full_model_8192_prompt_fused_matches_unfused(qwen3_8b_long):
         scale = float(u.float().abs().max())
         kv_noise = float((a.float() - u.float()).abs().max())
         assert float((u.float() - f.float()).abs().max()) <= max(2e-2 * scale, 2 * kv_noise)
-    assert sum(a == b for a, b in zip(tu, tf)) >= steps - 2, (tu, tf)
+    # Picks: the fused run is fed the unfused run's tokens, so its picks may part only where the unfused logits
+    # hold a near-tie, the margin between the two picks within twice that step's fused-unfused distance (N(0, 0.02)
+    # weights leave the top logits about 3% apart at this depth), and at most a sixth of the steps.
+    step_dev = (lf - lu).abs().amax(1)
+    for i, (a, b) in enumerate(zip(tu, tf)):
+        if a != b:
+            assert float(lu[i, a] - lu[i, b]) <= 2 * float(step_dev[i]) + 1e-6, (i, a, b)
+    assert sum(a == b for a, b in zip(tu, tf)) >= steps - steps // 6, (tu, tf)
     assert len(set(tu)) > 3
     del runs, ku, vu, kf, vf, ka, va
 
