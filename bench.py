@@ -12,8 +12,9 @@ Weights, cache and prompt are resident in HBM before timing starts.
 Prints one JSON line:
   value           decode tokens/s over K back-to-back graph replays: the median of --rounds
                   rounds (5), each from the state the prefill left; `spread` holds every
-                  round, the min and max, and the GPU's busy percentage read before timing
-                  (`contended` when above 10%); `host_cpu` the CPU model from /proc/cpuinfo
+                  round, the min and max, and the GPU's busy percentage read when the process
+                  starts, before it has run anything on the GPU (`contended` when above 10%:
+                  other work on the card); `host_cpu` the CPU model from /proc/cpuinfo
   roofline        the dominant kernel, the fused int8 GEMV (fused_gemv_kernel): the
                   step's own GEMV launches (egpt_qwen3_step_gemvs, 4 per layer + the
                   lm_head) replayed as one graph through egpt_int8_gemv_fused and timed
@@ -695,6 +696,7 @@ def main():
     cfg = QWEN3_1_7B if args.model == 'qwen3-1.7b' else QWEN3_8B
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
+    busy_at_start = gpu_busy_percent()  # before this process runs anything on the GPU
     n_stream = 256 if args.model == 'qwen3-1.7b' else 64
     cap = args.prompt + max(args.warmup + args.steps, n_stream) + 8
     t = time.perf_counter()
@@ -715,7 +717,6 @@ def main():
         # Rounds of the same workload: each restores the token and position the prefill left (the cache past the
         # prompt is rewritten by the round's own steps), replays W warm-up steps, then times K steps.
         token0, pos0 = eng.token.clone(), eng.position.clone()
-        busy_before = gpu_busy_percent()
         rounds = []
         for _ in range(max(1, args.rounds)):
             eng.token.copy_(token0)
@@ -739,8 +740,8 @@ def main():
                       'tok_s': [round(args.steps / r[0], 2) for r in rounds],
                       'median': round(value, 2), 'min': round(args.steps / walls[-1], 2),
                       'max': round(args.steps / walls[0], 2),
-                      'gpu_busy_percent_before': busy_before,
-                      'contended': None if busy_before is None else busy_before > 10.0}
+                      'gpu_busy_percent_at_start': busy_at_start,
+                      'contended': None if busy_at_start is None else busy_at_start > 10.0}
         mean_len = args.prompt + args.warmup + (args.steps + 1) / 2
 
         roof = gemv_roofline(eng)
