@@ -105,13 +105,15 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
 
 @pytest.mark.parametrize('shape,std,cap,plen', [(TINY, 0.2, 96, 9), (SMALL, 0.15, 96, 9), (SMALL, 0.15, 2048, 9),
                                                 (SMALL, 0.15, 2048, 1500), (TINY, 0.2, 4096, 9),
-                                                (SMALL8, 0.15, 96, 9), (SMALL8, 0.15, 2048, 1500),
-                                                (SMALL8, 0.15, 4096, 9)])
+                                                (TINY, 0.2, 8192, 9), (SMALL8, 0.15, 96, 9),
+                                                (SMALL8, 0.15, 2048, 1500), (SMALL8, 0.15, 4096, 9),
+                                                (SMALL8, 0.15, 4096, 3000)])
 def test_fused_step_matches_unfused_step(shape, std, cap, plen):
     """The fused step against the one-kernel-per-op step on the same tokens. Up to 2048 slots the attention blocks
     serve one query head and the o_proj GEMV merges their 2 or 8 splits (a 1500-token prompt fills the 8 splits of
-    a 2048-slot cache: about 190 slots each); at 4096 slots (32 splits, TINY 64) the blocks serve a kv head's whole
-    group and a launch of its own merges the splits. SMALL8 runs 4 query heads per kv head, as Qwen3-8B does."""
+    a 2048-slot cache: about 190 slots each); at 4096 slots (32 splits, TINY 64; 8192 slots, TINY 128) the blocks
+    serve a kv head's whole group and a launch of its own merges the splits, and a 3000-token prompt fills most of
+    the 32 splits. SMALL8 runs 4 query heads per kv head, as Qwen3-8B does."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
     prompt = torch.randint(0, shape.vocab, (plen,), generator=torch.Generator().manual_seed(3))
     runs = {}
@@ -230,12 +232,12 @@ def test_long_prompt_in_2048_slots_matches_oracle(shape):
     assert float((got - want).abs().max()) <= 2e-2 * float(want.abs().max())
 
 
-@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL8, 96), (SMALL, 2048), (SMALL8, 4096)])
+@pytest.mark.parametrize('shape,cap', [(SMALL, 96), (SMALL8, 96), (SMALL, 2048), (SMALL8, 4096), (TINY, 8192)])
 def test_fused_step_ignores_cache_past_position(shape, cap):
     """NaN in every cache slot past the position leaves the fused step's logits bit-identical: the reference's
     poisoning test of its split kernel (research/phase5/test_graph_gpu.py:250-261) run on the whole step, through
     the o_proj merge (2 and 8 splits) with attention blocks of one query head, and the separate merge launch (32
-    splits) with blocks of a kv head's whole group."""
+    and 128 splits) with blocks of a kv head's whole group."""
     eng, _ = build(shape, seed=13, std=0.15, cap=cap)
     prompt = torch.randint(0, shape.vocab, (9,), generator=torch.Generator().manual_seed(4))
     runs = []
