@@ -10,16 +10,18 @@
 // its fragments to bf16 in registers, so the weights cross HBM once, as int8.
 //
 // Design:
-//   * A block of 4 wavefronts (2 x 2) computes a BM x BN tile of y; a wavefront
-//     owns (BM / 2) x (BN / 2) as 32 x 32 tiles of v_mfma_f32_32x32x16_bf16
-//     (fp32 accumulators, bf16 products exact).
-//   * K advances 64 at a time through two LDS buffers: the global loads of step
-//     k + 1 are issued before the MFMAs of step k and written to LDS after them;
-//     one barrier per step.
-//   * x rows sit in LDS as bf16 (64 + 8 padding, 144 bytes); weight rows stay int8
-//     (64 + 16 padding, 80 bytes) and a wavefront converts each 8-byte fragment
-//     to bf16 after reading it, so the weights cost half the LDS traffic. The
-//     padding puts the fragment reads of 16 consecutive rows on distinct banks.
+//   * A block of 4 or 8 wavefronts computes a BM x BN tile of y; each wavefront
+//     owns a grid of 32 x 32 tiles of v_mfma_f32_32x32x16_bf16 (fp32
+//     accumulators, bf16 products exact).
+//   * K advances 64 (128 in the split slices) at a time through two LDS buffers
+//     and two register staging sets: the global loads of step k + 2 are issued
+//     before the MFMAs of step k; one barrier per step.
+//   * x rows sit in LDS as bf16 (BK + 8 padding). Weights are converted to bf16
+//     once per block by the thread that loaded them, as it writes them to LDS (the
+//     tiles with two wavefronts along M, which read the same fragments), or stay
+//     int8 (BK + 16 padding) and each wavefront converts the 8-byte fragments it
+//     reads (the 128 x 256 tile, whose wavefronts lie along N). The padding puts
+//     the fragment reads of 16 consecutive rows on distinct banks.
 //   * int8 -> bf16 is exact: every value in [-127, 127] is a bf16.
 //   * Rows past M or N read a valid row and are never stored.
 //   * Split-K (short M, long K: too few output tiles to give every CU a block):
@@ -135,14 +137,23 @@ __device__ __forceinline__ void gemm_tile(int b, int tiles_m, int tiles_n, int& 
   pid_n = (t % group) / gm;
 }
 
-template <int BM, int BN, int BK, bool SPLIT, int WN, int NW, bool SWIGLU = false>
+// BF16B: the weights are converted to bf16 once, by the thread that loaded them,
+// as they are written to LDS, and the wavefronts read bf16 fragments; otherwise
+// they stay int8 in LDS and every wavefront converts the fragments it reads (the
+// wavefronts along M convert the same fragment each). BF16B doubles the weights'
+// LDS space and read bytes.
+template <int BM, int BN, int BK, bool SPLIT, int WN, int NW, bool SWIGLU = false, bool BF16B = false>
 __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8_gemm_kernel(const GemmArgs a) {
   using S = GemmShape<BM, BN, BK, WN, NW>;
   constexpr int TM = S::TM, TN = S::TN;
   static_assert(!SWIGLU || (!SPLIT && TN % 2 == 0), "the SwiGLU form pairs a wavefront's column tiles");
   constexpr int kLdsRow = S::kLdsRow, kLdsRowW = S::kLdsRowW;
+  // weight row pitch in LDS: bytes (int8) or bf16 elements (BF16B, the x rows' pitch)
+  constexpr int kBRow = BF16B ? kLdsRow : kLdsRowW;
   __shared__ __align__(16) uint16_t As[2][BM * kLdsRow];
-  __shared__ __align__(16) int8_t Bs[2][BN * kLdsRowW];
+  __shared__ __align__(16) char Bsm[2][BF16B ? BN * kLdsRow * 2 : BN * kLdsRowW];
+  int8_t(&Bs)[2][BN * kLdsRowW] = *reinterpret_cast<int8_t(*)[2][BN * kLdsRowW]>(&Bsm);
+  uint16_t(&Bs16)[2][BN * kLdsRow] = *reinterpret_cast<uint16_t(*)[2][BN * kLdsRow]>(&Bsm);
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -178,7 +189,7 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
     const int row = i / (BK / 16), chunk = i % (BK / 16);
     const int64_t wrow = SWIGLU ? swiglu_row<BN, WN>(pid_n, row, a.inter) : min(n0 + row, (int64_t)a.N - 1);
     woff[j] = (uint32_t)(wrow * a.ldw + kbeg + chunk * 16);
-    b_lds[j] = row * kLdsRowW + chunk * 16;
+    b_lds[j] = row * kBRow + chunk * 16;
   }
   // Two register staging sets: the loads of step k + 2 are issued while step k is
   // multiplied and land in LDS at the end of step k + 1, about two steps of MFMA
@@ -197,7 +208,14 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
 #pragma unroll
     for (int j = 0; j < S::kALoads; ++j) *(u32x4*)&As[buf][a_lds[j]] = xr[set][j];
 #pragma unroll
-    for (int j = 0; j < S::kBLoads; ++j) *(u32x4*)&Bs[buf][b_lds[j]] = wr[set][j];
+    for (int j = 0; j < S::kBLoads; ++j) {
+      if constexpr (BF16B) {
+        *(bf16x8*)&Bs16[buf][b_lds[j]] = int8x8_to_bf16(wr[set][j].x, wr[set][j].y);
+        *(bf16x8*)&Bs16[buf][b_lds[j] + 8] = int8x8_to_bf16(wr[set][j].z, wr[set][j].w);
+      } else {
+        *(u32x4*)&Bs[buf][b_lds[j]] = wr[set][j];
+      }
+    }
   };
 
   f32x16 acc[TM][TN];
@@ -212,7 +230,7 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) a_frag[tm] = (wm0 + tm * 32 + lane % 32) * kLdsRow + frag_k;
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) b_frag[tn] = (wn0 + tn * 32 + lane % 32) * kLdsRowW + frag_k;
+  for (int tn = 0; tn < TN; ++tn) b_frag[tn] = (wn0 + tn * 32 + lane % 32) * kBRow + frag_k;
 
   // The MFMAs of one K step from LDS buffer `buf`, 16 K columns at a time.
   auto mma_step = [&](int buf) {
@@ -222,22 +240,28 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
       // of the step first, then convert and multiply.
       bf16x8 af[BK / 16][TM];
       uint32_t bw[BK / 16][TN][2];
+      bf16x8 bh[BK / 16][TN];
 #pragma unroll
       for (int ks = 0; ks < BK / 16; ++ks) {
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) af[ks][tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-          const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
-          bw[ks][tn][0] = p[0];
-          bw[ks][tn][1] = p[1];
+          if constexpr (BF16B) {
+            bh[ks][tn] = *(const bf16x8*)&Bs16[buf][b_frag[tn] + ks * 16];
+          } else {
+            const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
+            bw[ks][tn][0] = p[0];
+            bw[ks][tn][1] = p[1];
+          }
         }
       }
 #pragma unroll
       for (int ks = 0; ks < BK / 16; ++ks) {
         bf16x8 bfr[TN];
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) bfr[tn] = int8x8_to_bf16(bw[ks][tn][0], bw[ks][tn][1]);
+        for (int tn = 0; tn < TN; ++tn)
+          bfr[tn] = BF16B ? bh[ks][tn] : int8x8_to_bf16(bw[ks][tn][0], bw[ks][tn][1]);
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -252,8 +276,12 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
         for (int tm = 0; tm < TM; ++tm) af[tm] = *(const bf16x8*)&As[buf][a_frag[tm] + ks * 16];
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-          const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
-          bfr[tn] = int8x8_to_bf16(p[0], p[1]);
+          if constexpr (BF16B) {
+            bfr[tn] = *(const bf16x8*)&Bs16[buf][b_frag[tn] + ks * 16];
+          } else {
+            const uint32_t* p = (const uint32_t*)&Bs[buf][b_frag[tn] + ks * 16];
+            bfr[tn] = int8x8_to_bf16(p[0], p[1]);
+          }
         }
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
@@ -389,6 +417,11 @@ unsigned gemm_blocks(const GemmArgs& a) {
 
 constexpr int kMaxSplits = 16;
 
+// Tiles whose weights go to LDS as bf16 (converted once per block, int8_gemm_kernel's BF16B).
+template <int BM, int BN>
+constexpr bool kBf16B = (BM == 64 && BN == 64) || (BM == 128 && BN == 64) || (BM == 128 && BN == 128) ||
+                        (BM == 256 && BN == 256);
+
 // The reduce for a.splits (2 ... S) slices; false for a count outside that range.
 template <int S>
 bool launch_reduce(const GemmArgs& a, unsigned blocks, hipStream_t st) {
@@ -407,8 +440,8 @@ int launch_split_partials(GemmArgs a, hipStream_t st) {
   a.tiles_m = (int)(((int64_t)a.M + 63) / 64);
   a.tiles_n = (int)(((int64_t)a.N + 63) / 64);
   const unsigned tiles = (unsigned)a.tiles_m * (unsigned)a.tiles_n;
-  hipLaunchKernelGGL((int8_gemm_kernel<64, 64, kBKSplit, true, 2, 4>), dim3(tiles * (unsigned)a.splits),
-                     dim3(4 * kWave), 0, st, a);
+  hipLaunchKernelGGL((int8_gemm_kernel<64, 64, kBKSplit, true, 2, 4, false, kBf16B<64, 64>>),
+                     dim3(tiles * (unsigned)a.splits), dim3(4 * kWave), 0, st, a);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -426,7 +459,8 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
       return EGPT_LAUNCH_STATUS();
     }
   }
-  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false, WN, NW>), dim3(tiles), dim3(NW * kWave), 0, st, a);
+  hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false, WN, NW, false, kBf16B<BM, BN>>), dim3(tiles),
+                     dim3(NW * kWave), 0, st, a);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -559,7 +593,7 @@ extern "C" int egpt_int8_gemm_swiglu(const void* x, int64_t ldx, const int8_t* w
   if (M > 128 && blocks(256, 256) >= 256) {
     a.tiles_m = (M + 255) / 256;
     a.tiles_n = (inter + 127) / 128;
-    hipLaunchKernelGGL((int8_gemm_kernel<256, 256, kBK, false, kWN256x256, kNW256x256, true>),
+    hipLaunchKernelGGL((int8_gemm_kernel<256, 256, kBK, false, kWN256x256, kNW256x256, true, kBf16B<256, 256>>),
                        dim3((unsigned)(a.tiles_m * a.tiles_n)), dim3(kNW256x256 * kWave), 0, stream, a);
     return EGPT_LAUNCH_STATUS();
   }

@@ -527,6 +527,9 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma_lds(
       }
     }
   }
+  // the two chunks issued past the last one land in this block's LDS: wait for them
+  // before the block ends and its LDS goes to another
+  EGPT_WAIT_VMCNT(0);
 }
 
 template <int G, int FG>
