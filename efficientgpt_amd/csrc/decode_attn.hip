@@ -98,6 +98,10 @@ __global__ __launch_bounds__(NT) void attn_split_kernel(
 }
 
 // Partial-softmax reduce: one block of kCombineThreads per (b, query head).
+// Block c takes (row, kv head) group p = c % P (P = B * Hkv groups) and query
+// head c / P of that group's G: blocks are dispatched round-robin to the 8 XCDs,
+// so with P a multiple of 8 it runs on the XCD whose L2 took the group's partials
+// (split block (p, split) has linear index split * P + p).
 constexpr int kCombineThreads = 256;
 
 template <typename T, int D>
@@ -105,10 +109,13 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(const flo
                                                                        const float* __restrict__ ws_l,
                                                                        const float* __restrict__ ws_acc,
                                                                        T* __restrict__ out, int64_t o_sb, int64_t o_sh,
-                                                                       int Hq, int nsplit) {
-  const int bh = blockIdx.x;
-  const int b = bh / Hq;
-  const int h = bh % Hq;
+                                                                       int Hq, int Hkv, int nsplit) {
+  const int G = Hq / Hkv;
+  const int P = (int)gridDim.x / G;
+  const int p = (int)blockIdx.x % P;
+  const int b = p / Hkv;
+  const int h = (p % Hkv) * G + (int)blockIdx.x / P;
+  const int bh = b * Hq + h;
   float r;
   if (attn_combine_block<D, kCombineThreads>(ws_m + (int64_t)bh * nsplit, ws_l + (int64_t)bh * nsplit,
                                              ws_acc + (int64_t)bh * nsplit * D, nsplit, r))
@@ -137,7 +144,7 @@ int launch_attn(const AttnArgs& a, hipStream_t st) {
   if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
   if (a.nsplit == 1) return EGPT_OK;  // the split kernel wrote the output
   hipLaunchKernelGGL((attn_combine_kernel<T, D>), dim3((unsigned)(a.B * a.Hq)), dim3(kCombineThreads), 0, st,
-                     a.ws_m, a.ws_l, a.ws_acc, (T*)a.out, a.o_sb, a.o_sh, a.Hq, a.nsplit);
+                     a.ws_m, a.ws_l, a.ws_acc, (T*)a.out, a.o_sb, a.o_sh, a.Hq, a.Hkv, a.nsplit);
   return EGPT_LAUNCH_STATUS();
 }
 
