@@ -292,8 +292,8 @@ class Qwen3Int8Engine:
         d.x, d.qkv, d.attn, d.act, d.logits = ptr(self.x), ptr(self.qkv), ptr(self.attn), ptr(self.act), ptr(self.logits)
         need = ctypes.c_size_t()
         _lib.check('egpt_qwen3_step_workspace', lib.egpt_qwen3_step_workspace(ctypes.byref(d), ctypes.byref(need)))
-        # zeroed once: the kernels' hand-off counters start at zero and are returned to zero by the kernels
-        self.step_ws = torch.zeros(need.value, device=self.device, dtype=torch.uint8)
+        # attention partials and argmax partials: every step writes them before it reads them
+        self.step_ws = torch.empty(need.value, device=self.device, dtype=torch.uint8)
         d.workspace, d.workspace_bytes = ptr(self.step_ws), need.value
         if self._ring_dev:
             d.token_ring, d.token_ring_slots = self._ring_dev, self.cap

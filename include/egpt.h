@@ -325,8 +325,9 @@ int egpt_argmax_parts(const float *part_v, const int *part_i, int parts, int64_t
  * rope_cos / rope_sin bf16 [cap, head_dim]; x / qkv / attn / act / logits are
  * bf16 rows of hidden / (heads + 2 kv_heads) head_dim / heads head_dim / inter /
  * vocab elements (logits may be NULL). `layer` is a HOST array of `layers` entries.
- * The workspace (egpt_qwen3_step_workspace bytes, 256-byte aligned) must be zeroed
- * once before the first step; the kernels return its counters to zero.
+ * The workspace (egpt_qwen3_step_workspace bytes, 256-byte aligned) holds the
+ * attention and argmax partials; every step writes them before reading them, so
+ * its contents on entry do not matter.
  * Sizes: hidden, inter and heads*head_dim multiples of 16 and <= 12288;
  * head_dim in {32, 64, 128}; heads / kv_heads in {1, 2, 4, 8}.
  */
