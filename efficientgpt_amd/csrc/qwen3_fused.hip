@@ -657,8 +657,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
   constexpr int LPS = Geo::LPS;
   const int tid = threadIdx.x;
   const int d0 = (tid % LPS) * EPL;
-  const int hq0 = blockIdx.x * G;
-  const int hk = hq0 / a.group;
+  // Block column x serves query heads hq0 .. hq0 + G - 1 of kv head x mod Hkv:
+  // the columns of one kv head are x, x + Hkv, ..., so with Hkv a multiple of 8
+  // they all run on one XCD (blocks go round-robin to the 8 XCDs) and the kv
+  // head's K/V rows, read once per column, come from that XCD's L2 after the first.
+  const int hk = (int)blockIdx.x % a.Hkv;
+  const int hq0 = hk * a.group + ((int)blockIdx.x / a.Hkv) * G;
   const int split = blockIdx.y;
   const int Hq = a.Hkv * a.group;
 
@@ -773,19 +777,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_step_kernel(const AttnStep 
 }
 
 // Merge of the split partials: one block per query head. The attention launch's
-// block column x (of X = Hq / G, G query heads per block) ran every split of
-// heads x G .. x G + G - 1 on one XCD (x mod 8, blocks being dispatched
-// round-robin to the 8 XCDs) when X is a multiple of 8; merge block c takes head
-// (c mod X) G + c / X, so it runs on that XCD and finds the partials in its L2.
+// block column x (of X = Hq / G, G query heads per block) ran every split of its
+// heads (from (x mod Hkv) group + (x / Hkv) G on) on one XCD (x mod 8, blocks
+// being dispatched round-robin to the 8 XCDs) when X is a multiple of 8; merge
+// block c takes head j = c / X of column c mod X, so it runs on that XCD and finds
+// the partials in its L2.
 constexpr int kMergeThreads = 256;
 
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict__ ws_m,
                                                                    const float* __restrict__ ws_l,
                                                                    const float* __restrict__ ws_acc,
-                                                                   uint16_t* __restrict__ out, int nsplit, int G) {
+                                                                   uint16_t* __restrict__ out, int nsplit, int G,
+                                                                   int Hkv) {
   const int X = (int)gridDim.x / G;
-  const int h = ((int)blockIdx.x % X) * G + (int)blockIdx.x / X;
+  const int x = (int)blockIdx.x % X;
+  const int h = (x % Hkv) * (X / Hkv * G) + (x / Hkv) * G + (int)blockIdx.x / X;
   float r;
   if (attn_combine_block<D, kMergeThreads>(ws_m + (int64_t)h * nsplit, ws_l + (int64_t)h * nsplit,
                                            ws_acc + (int64_t)h * nsplit * D, nsplit, r))
@@ -919,7 +926,7 @@ int launch_attn_step(const AttnStep& a, int G, uint16_t* out, bool merge, hipStr
   if (hipGetLastError() != hipSuccess) return EGPT_ERR_LAUNCH;
   if (merge)
     hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((unsigned)(a.Hkv * a.group)), dim3(kMergeThreads), 0, st, a.ws_m,
-                       a.ws_l, a.ws_acc, out, a.nsplit, G);
+                       a.ws_l, a.ws_acc, out, a.nsplit, G, a.Hkv);
   return EGPT_LAUNCH_STATUS();
 }
 
