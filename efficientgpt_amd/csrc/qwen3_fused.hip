@@ -635,11 +635,13 @@ struct AttnStep {
 // holds at most this many slots, and a whole kv head's group of query heads
 // (reading its K/V once) past it. Short caches are latency-bound: a block with
 // one head finishes its loop and its merge sooner, and reading each K/V row once
-// per query head costs little. Measured on the MI355X, with the split counts of
-// egpt_qwen3_step_default_splits, against whole-group blocks: Qwen3-1.7B (2
-// query heads per kv head) 4.9% faster at 392 slots and 4.5-5.4% at 1264-1764,
-// Qwen3-8B (4) 5.7% and 2.6-3.3%; at 3.3k-3.8k slots both 4.5-5% slower.
-constexpr int kHeadBlockMaxSlots = 2048;
+// per query head costs little (the columns of one kv head share an XCD, so after
+// the first the group's reads of a K/V row come from L2). Measured on the MI355X,
+// with the split counts of egpt_qwen3_step_default_splits, against whole-group
+// blocks: Qwen3-1.7B (2 query heads per kv head) 4.9% faster at 392 slots,
+// 4.5-5.4% at 1264-1764 and 0.6-2.2% at 2264-3064, Qwen3-8B (4) 5.7%, 2.6-3.3% and
+// 1.3-2.6% (at 2580-2980); at 3.8k slots the 1.7B 2.7% slower.
+constexpr int kHeadBlockMaxSlots = 3072;
 
 // Attention partials of one decode step: block (query heads hq0 .. hq0 + G - 1
 // of one kv head, split). Every load that does not depend on arithmetic is
@@ -1168,9 +1170,9 @@ extern "C" int egpt_argmax_parts(const float* part_v, const int* part_i, int par
 extern "C" int egpt_qwen3_step_default_splits(int heads, int kv_heads, int head_dim, int cap) {
   if (heads < 1 || kv_heads < 1 || head_dim < 1 || cap < 1) return 1;
   const int by_len = (cap + 63) / 64;
-  // Attention blocks of one query head (kHeadBlockMaxSlots): at most 4 splits up
-  // to 512 slots and 8 past that, so the o_proj prologue merges them at its
-  // 4- or 8-split bound. Measured on the MI355X against about one block per CU
+  // Attention blocks of one query head (up to kHeadBlockMaxSlots): at most 4
+  // splits up to 512 slots and 8 past that, so the o_proj prologue merges them at
+  // its 4- or 8-split bound (16 splits past 2048 slots measured 1-6% slower). Measured on the MI355X against about one block per CU
   // (7, 11, 16 and 16 splits at 392, 664, 964 and 1764 slots): Qwen3-1.7B 1.9%,
   // 5.8%, 3% and 4.5% faster, Qwen3-8B 1.7%, 6% and 3.3% at 392, 964 and 1764.
   if (cap <= kHeadBlockMaxSlots) {

@@ -377,10 +377,10 @@ typedef struct egpt_qwen3_step {
 } egpt_qwen3_step;
 
 int egpt_qwen3_step_workspace(const egpt_qwen3_step *step, size_t *bytes);
-/* The step's split count for `nsplit`. Up to 2048 slots, where the step's
+/* The step's split count for `nsplit`. Up to 3072 slots, where the step's
  * attention blocks serve one query head each: one split per 64 slots, at most 4
  * up to 512 slots and 8 past that, merged in the o_proj GEMV's prologue. Past
- * 2048 slots (blocks of a kv head's whole group): about one block per CU and at
+ * 3072 slots (blocks of a kv head's whole group): about one block per CU and at
  * least 64 slots per split, merged in one small launch past 16. Unlike the
  * stand-alone attention, the step splits short caches too, since its merge needs
  * no launch of its own. Has no counterpart in the reference, whose step reads

@@ -80,12 +80,12 @@ def test_split_policies():
             if cap > 256:
                 assert n == min(-(-cap // 64), -(-256 // (b * hkv)), 256), (b, hkv, cap, n)
     step = lib.egpt_qwen3_step_default_splits
-    # Qwen3-1.7B geometry (16 / 8 heads, D 128): up to 2048 slots (attention blocks of one query head) at most 4
+    # Qwen3-1.7B geometry (16 / 8 heads, D 128): up to 3072 slots (attention blocks of one query head) at most 4
     # splits to 512 slots and 8 past that; then about one block per CU
-    assert [step(16, 8, 128, c) for c in (64, 96, 256, 400, 512, 513, 1024, 1772, 2048, 2049, 32768)] == \
-        [1, 2, 4, 4, 4, 8, 8, 8, 8, 32, 32]
+    assert [step(16, 8, 128, c) for c in (64, 96, 256, 400, 512, 513, 1024, 1772, 2048, 3072, 3073, 32768)] == \
+        [1, 2, 4, 4, 4, 8, 8, 8, 8, 8, 32, 32]
     # Qwen3-8B geometry (32 / 8 heads)
-    assert [step(32, 8, 128, c) for c in (400, 964, 1772, 2048, 2112, 8192)] == [4, 8, 8, 8, 32, 32]
+    assert [step(32, 8, 128, c) for c in (400, 964, 1772, 2048, 2112, 3072, 3136, 8192)] == [4, 8, 8, 8, 8, 8, 32, 32]
     assert step(4, 2, 32, 4096) == 64
     assert step(0, 8, 128, 100) == 1 and step(16, 0, 128, 100) == 1
 

@@ -107,11 +107,12 @@ def test_graph_decoder_greedy_matches_oracle(shape, std):
                                                 (SMALL, 0.15, 2048, 1500), (TINY, 0.2, 4096, 9),
                                                 (TINY, 0.2, 8192, 9), (SMALL8, 0.15, 96, 9),
                                                 (SMALL8, 0.15, 2048, 1500), (SMALL8, 0.15, 4096, 9),
-                                                (SMALL8, 0.15, 4096, 3000)])
+                                                (SMALL8, 0.15, 4096, 3000), (SMALL, 0.15, 3072, 2900),
+                                                (SMALL8, 0.15, 3072, 2900)])
 def test_fused_step_matches_unfused_step(shape, std, cap, plen):
-    """The fused step against the one-kernel-per-op step on the same tokens. Up to 2048 slots the attention blocks
+    """The fused step against the one-kernel-per-op step on the same tokens. Up to 3072 slots the attention blocks
     serve one query head and the o_proj GEMV merges their 2 or 8 splits (a 1500-token prompt fills the 8 splits of
-    a 2048-slot cache: about 190 slots each); at 4096 slots (32 splits, TINY 64; 8192 slots, TINY 128) the blocks
+    a 2048-slot cache: about 190 slots each; a 2900-token prompt 8 of about 360 in a 3072-slot cache); at 4096 slots (32 splits, TINY 64; 8192 slots, TINY 128) the blocks
     serve a kv head's whole group and a launch of its own merges the splits, and a 3000-token prompt fills most of
     the 32 splits. SMALL8 runs 4 query heads per kv head, as Qwen3-8B does."""
     eng, _ = build(shape, seed=11, std=std, cap=cap)
