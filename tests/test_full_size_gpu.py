@@ -29,7 +29,7 @@ tokens with generate's (research/realmodel/test_fast_decode.py:26-40) on a tiny
 model, where rounding never
 decides a pick; the tiny-model tests here keep its exact-match bar.
 
-The north star's bars as written (at least 99% greedy agreement, logits within 2e-2) are then checked at full
+The fixed parity bars (at least 99% greedy-token agreement, logits within 2e-2 of the top logit) are then checked at full
 depth on a model whose picks the weights decide (decisive_qwen3_1p7b: 28 layers at the 1.7B widths, a strong
 token embedding and small residual projections, a vocabulary cut to 8192 rows), as the reference's decoder test
 makes its tiny model decisive with initializer_range 0.2; the test measures that the median top-1 / top-2 margin
@@ -183,7 +183,7 @@ def decisive_qwen3_1p7b(vocab=8192, seed=0):
 
 
 def test_qwen3_1p7b_depth_decisive_model_meets_the_fixed_bars():
-    """The north star's bars as written, at full depth: 28 layers at Qwen3-1.7B widths (vocabulary cut to 8192),
+    """The fixed parity bars, at full depth: 28 layers at Qwen3-1.7B widths (vocabulary cut to 8192),
     a 128-token prompt and 256 greedy tokens through GraphGreedyDecoder, every step teacher-forced against the
     oracle: at least 99% of the picks equal the oracle's, and every step's logits lie within 2e-2 of the step's
     top logit. The weights (decisive_qwen3_1p7b) make the picks decided by the model, as the reference's decoder
