@@ -674,7 +674,7 @@ def dispatch_grid(inner=20, reps=20):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({'error': 'this build measures one GPU; runs on several GPUs are not part of it',
+        print(json.dumps({'error': 'bench.py measures one GPU; runs on several GPUs are not supported',
                           'n_gpus': args.gpus}), flush=True)
         sys.exit(2)
     if args.dispatch_grid:
