@@ -23,11 +23,12 @@ were checked when it ran eagerly). Every layer of one forward receives the same
 position_ids tensor, so the host read is made once per forward: the result is kept
 for that tensor object while its contents are unchanged (its version counter).
 
-Several queries per row (a prompt): more than PREFILL_KERNEL_MAX_ROWS bf16 queries
-take the causal prompt-attention kernel (egpt_prefill_attn: query t at position
+Several queries per row (a prompt): bf16 queries that the engine's rule
+(qwen3.use_prompt_kernel: more than 64 rows reaching past position 160) gives to the
+causal prompt-attention kernel take it (egpt_prefill_attn: query t at position
 pos0 + t attends slots 0..pos0 + t, one pass over the prefix per block of queries);
-fewer, or other dtypes, run as a batch of single queries of the split-K decode
-kernel over the same cache (batch stride 0), query t attending slots
+the others, and other dtypes, run as a batch of single queries of the split-K
+decode kernel over the same cache (batch stride 0), query t attending slots
 0..position_ids[b, t].
 """
 
@@ -37,10 +38,9 @@ import torch
 
 from . import _lib
 from .decode_attention import _run
+from .qwen3 import use_prompt_kernel
 
 NAME = 'egpt_decode'
-# Prompts longer than this take the prompt-attention kernel (the engine's rule, qwen3.PREFILL_KERNEL_MAX_ROWS).
-PREFILL_KERNEL_MAX_ROWS = 64
 
 # The last position_ids / mask that passed the host check: (position_ids ref, its version, mask ref or None, mask
 # version, (B, T, cap), host positions [B, T]).
@@ -146,7 +146,7 @@ def egpt_attention(module, query, key, value, attention_mask, scaling=None, drop
     scale = scaling if scaling is not None else d ** -0.5
     outs = []
     for row in range(b):
-        if t > PREFILL_KERNEL_MAX_ROWS and host is not None and query.dtype == torch.bfloat16:
+        if host is not None and query.dtype == torch.bfloat16 and use_prompt_kernel(t, int(host[row, 0])):
             o = _prompt_rows(query, key, value, row, int(host[row, 0]), scale)
             if o is not None:
                 outs.append(o)

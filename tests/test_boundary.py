@@ -131,3 +131,12 @@ def test_hf_adapter_checks_each_position_tensor_once_and_rechecks_changes():
     pos[0, 0] = 0  # written in place: its version moves, so the padded positions are caught
     with pytest.raises(ValueError, match='consecutive'):
         hf.query_slots(q, k, None, pos)
+
+
+def test_prompt_attention_rule():
+    """Which prompts take the causal prompt kernel: more than 64 rows whose last position reaches past 160; every
+    other prompt runs the split-K decode kernel over its rows (host rule, no GPU)."""
+    from efficientgpt_amd.qwen3 import use_prompt_kernel
+    assert not use_prompt_kernel(64, 0) and not use_prompt_kernel(64, 8000)
+    assert not use_prompt_kernel(128, 0) and not use_prompt_kernel(160, 0) and not use_prompt_kernel(100, 60)
+    assert use_prompt_kernel(161, 0) and use_prompt_kernel(65, 96) and use_prompt_kernel(8192, 0)

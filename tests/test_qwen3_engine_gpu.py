@@ -50,9 +50,9 @@ def oracle_greedy_with_margins(orc, prompt, n):
 
 @pytest.mark.parametrize('shape,std', [(TINY, 0.2), (SMALL, 0.15)])
 def test_prefill_logits_match_oracle(shape, std):
-    eng, orc = build(shape, seed=1, std=std, cap=160)
+    eng, orc = build(shape, seed=1, std=std, cap=224)
     g = torch.Generator().manual_seed(2)
-    for p in (1, 5, 17, 37, 100):  # 100 rows: the long-prompt attention path
+    for p in (1, 5, 17, 37, 100, 200):  # 100 rows: the decode kernel over the prompt; 200: the prompt kernel
         prompt = torch.randint(0, shape.vocab, (p,), generator=g)
         eng.reset()
         got = eng.prefill(prompt).float().cpu()
@@ -387,7 +387,8 @@ def test_transformers_model_int8_through_graph_decoder():
 
 def test_hf_attention_adapter_matches_oracle_attention():
     """transformers with attn_implementation 'egpt_decode' (the HIP kernel) vs the fp32 oracle attention. The
-    100-token prompt is past PREFILL_KERNEL_MAX_ROWS: its prefill runs the prompt-attention kernel at head dim 32."""
+    100-token prompt runs the split-K decode kernel over its rows; the 170-token one is past the decode kernel's
+    context bound (qwen3.use_prompt_kernel): its prefill runs the prompt-attention kernel at head dim 32."""
     transformers = pytest.importorskip('transformers')
     from efficientgpt_amd import hf
     hf.register()
@@ -398,10 +399,10 @@ def test_hf_attention_adapter_matches_oracle_attention():
                                    attn_implementation=hf.NAME)
     model = transformers.Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
     sd = {k: v.clone() for k, v in model.state_dict().items()}
-    orc = Qwen3Oracle(TINY, sd, dtype=torch.bfloat16, cap=128, inv_freq=model.model.rotary_emb.inv_freq)
+    orc = Qwen3Oracle(TINY, sd, dtype=torch.bfloat16, cap=256, inv_freq=model.model.rotary_emb.inv_freq)
     model = model.cuda()
     g = torch.Generator().manual_seed(4)
-    for p in (1, 6, 30, 100):
+    for p in (1, 6, 30, 100, 170):
         x = torch.randint(0, 512, (1, p), generator=g)
         with torch.no_grad():
             got = model.generate(input_ids=x.cuda(), attention_mask=torch.ones_like(x).cuda(), max_new_tokens=20,
