@@ -22,6 +22,10 @@ HIPCC_FLAGS = [
     # they are switched off for every kernel. The host pass warns that it does not
     # know the feature; that is expected.
     '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    # Leading scalar and pointer kernel arguments are preloaded into registers at
+    # launch (gfx950 kernel-argument preload), so a kernel's first loads need no
+    # read of its argument block; structs passed by value are not preloaded.
+    '-mllvm', '-amdgpu-kernarg-preload-count=16',
     '-Wno-unused-command-line-argument',
     f'-I{ROOT / "include"}',
 ]
