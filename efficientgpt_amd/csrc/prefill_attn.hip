@@ -148,14 +148,18 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
       // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions
       const int p0 = (4 * vg) & ~15;
       const int p = p0 + vperm((4 * vg) & 15);
+      // dim 2 w + h of the four slots: the 16-bit half h of word w of each row,
+      // two slots per v_perm_b32 (bytes 0-1 or 2-3 of each source)
+      const uint32_t r0[4] = {sr[0].x, sr[0].y, sr[0].z, sr[0].w};
+      const uint32_t r1[4] = {sr[1].x, sr[1].y, sr[1].z, sr[1].w};
+      const uint32_t r2[4] = {sr[2].x, sr[2].y, sr[2].z, sr[2].w};
+      const uint32_t r3[4] = {sr[3].x, sr[3].y, sr[3].z, sr[3].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int sh = 16 * (e & 1);
-        const uint32_t w0 = ((e < 2 ? sr[0].x : e < 4 ? sr[0].y : e < 6 ? sr[0].z : sr[0].w) >> sh) & 0xffffu;
-        const uint32_t w1 = ((e < 2 ? sr[1].x : e < 4 ? sr[1].y : e < 6 ? sr[1].z : sr[1].w) >> sh) & 0xffffu;
-        const uint32_t w2 = ((e < 2 ? sr[2].x : e < 4 ? sr[2].y : e < 6 ? sr[2].z : sr[2].w) >> sh) & 0xffffu;
-        const uint32_t w3 = ((e < 2 ? sr[3].x : e < 4 ? sr[3].y : e < 6 ? sr[3].z : sr[3].w) >> sh) & 0xffffu;
-        *(uint2*)&Vs[buf][(vc * 8 + e) * kPfVRow + p] = make_uint2(w0 | (w1 << 16), w2 | (w3 << 16));
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const int w = e / 2;
+        *(uint2*)&Vs[buf][(vc * 8 + e) * kPfVRow + p] =
+            make_uint2(__builtin_amdgcn_perm(r1[w], r0[w], sel), __builtin_amdgcn_perm(r3[w], r2[w], sel));
       }
     }
   };
@@ -173,18 +177,17 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
     const int buf = j & 1;
     if (j + 1 < nt) gload(j + 1);
     // S^T for slots 64 j + 32 mt + (8 (r / 4) + 4 half + r % 4), query col
-    f32x16_pf st[2];
+    // (the two 32-slot halves are independent chains: interleaved, each MFMA's
+    // accumulator was written two MFMAs earlier)
+    f32x16_pf st[2] = {f32x16_pf{}, f32x16_pf{}};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      st[mt] = f32x16_pf{};
-      const uint16_t* kr0 = &Ks[buf][(32 * mt + col) * kPfKRow + 8 * half];
+    for (int kk = 0; kk < kPfD / 16; ++kk)
 #pragma unroll
-      for (int kk = 0; kk < kPfD / 16; ++kk) {
-        const u32x4 av = *(const u32x4*)(kr0 + 16 * kk);
+      for (int mt = 0; mt < 2; ++mt) {
+        const u32x4 av = *(const u32x4*)&Ks[buf][(32 * mt + col) * kPfKRow + 8 * half + 16 * kk];
         st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
                                                          __builtin_bit_cast(bf16x8_pf, qf[kk]), st[mt], 0, 0, 0);
       }
-    }
     // Online softmax of this lane's query over the tile's 64 slots (32 here, 32 in
     // lane ^ 32), in the units of the raw scores q . k: the scale is positive, so
     // the maximum commutes with it, and p = 2^((s - m) * scale * log2 e) takes one
@@ -238,9 +241,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
       const f32x16_pf& pt = st[js / 2];
       uint32_t pk[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        pk[e] = (uint32_t)f32_to_bf16(pt[8 * (js % 2) + 2 * e]) |
-                ((uint32_t)f32_to_bf16(pt[8 * (js % 2) + 2 * e + 1]) << 16);
+      for (int e = 0; e < 4; ++e) pk[e] = pack2_bf16(pt[8 * (js % 2) + 2 * e], pt[8 * (js % 2) + 2 * e + 1]);
       const bf16x8_pf pb = __builtin_bit_cast(bf16x8_pf, u32x4{pk[0], pk[1], pk[2], pk[3]});
       const uint16_t* vr0 = &Vs[buf][col * kPfVRow + 16 * js + 8 * half];
 #pragma unroll
@@ -261,10 +262,8 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
     for (int dt = 0; dt < kPfD / 32; ++dt)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const uint32_t lo = (uint32_t)f32_to_bf16(o[dt][4 * r4] * inv) |
-                            ((uint32_t)f32_to_bf16(o[dt][4 * r4 + 1] * inv) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16(o[dt][4 * r4 + 2] * inv) |
-                            ((uint32_t)f32_to_bf16(o[dt][4 * r4 + 3] * inv) << 16);
+        const uint32_t lo = pack2_bf16(o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv);
+        const uint32_t hi = pack2_bf16(o[dt][4 * r4 + 2] * inv, o[dt][4 * r4 + 3] * inv);
         *(uint2*)(orow + 32 * dt + 8 * r4) = make_uint2(lo, hi);
       }
   }
