@@ -15,8 +15,9 @@
 // A block is 8 wavefronts over one kv head; each wavefront owns 32 consecutive
 // query rows of one query head, so a block covers min(group, 4) query heads and
 // 32 * 8 / min(group, 4) positions, and every head of the block shares the K/V
-// tiles it stages. K/V advance 64 slots at a time through two LDS buffers (the
-// global loads of tile j + 1 are issued before tile j is multiplied).
+// tiles it stages. K/V advance 64 slots at a time through three LDS buffers (the
+// global loads of tile j + 1 are issued before tile j is multiplied; wavefronts
+// 4-7 run a phase behind 0-3 and read tile j - 1's V during tile j).
 //
 // Per tile and wavefront, with v_mfma_f32_32x32x16_bf16 (lane l holds A[l % 32]
 // [8 (l / 32) + e] and B[8 (l / 32) + e][l % 32]; accumulator register r of lane
@@ -73,8 +74,8 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
   constexpr int kPfKRow = kPfD + 8;     // bf16 per K row in LDS (16 bytes of padding)
   constexpr int kChunks = kPfD / 8;     // 16-byte chunks per K/V row
   constexpr int kLoads = kChunks / 4;   // 16-byte loads per staging thread and tile: 64 slots x kChunks / 256
-  __shared__ __align__(16) uint16_t Ks[2][kPfSlots * kPfKRow];
-  __shared__ __align__(16) uint16_t Vs[2][kPfD * kPfVRow];
+  __shared__ __align__(16) uint16_t Ks[3][kPfSlots * kPfKRow];
+  __shared__ __align__(16) uint16_t Vs[3][kPfD * kPfVRow];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -169,30 +170,28 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
   for (int dt = 0; dt < kPfD / 32; ++dt) o[dt] = f32x16_pf{};
   float m = -INFINITY, l = 0.f;
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-#pragma unroll 1
-  for (int j = 0; j < nt; ++j) {
-    const int buf = j & 1;
-    if (j + 1 < nt) gload(j + 1);
-    // S^T for slots 64 j + 32 mt + (8 (r / 4) + 4 half + r % 4), query col
-    // (the two 32-slot halves are independent chains: interleaved, each MFMA's
-    // accumulator was written two MFMAs earlier)
-    f32x16_pf st[2] = {f32x16_pf{}, f32x16_pf{}};
+  // S^T for slots 64 j + 32 mt + (8 (r / 4) + 4 half + r % 4), query col, from
+  // the K tile in LDS buffer b (the two 32-slot halves are independent chains:
+  // interleaved, each MFMA's accumulator was written two MFMAs earlier).
+  auto qk = [&](int b, f32x16_pf (&st)[2]) {
+    st[0] = f32x16_pf{};
+    st[1] = f32x16_pf{};
 #pragma unroll
     for (int kk = 0; kk < kPfD / 16; ++kk)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const u32x4 av = *(const u32x4*)&Ks[buf][(32 * mt + col) * kPfKRow + 8 * half + 16 * kk];
+        const u32x4 av = *(const u32x4*)&Ks[b][(32 * mt + col) * kPfKRow + 8 * half + 16 * kk];
         st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
                                                          __builtin_bit_cast(bf16x8_pf, qf[kk]), st[mt], 0, 0, 0);
       }
-    // Online softmax of this lane's query over the tile's 64 slots (32 here, 32 in
-    // lane ^ 32), in the units of the raw scores q . k: the scale is positive, so
-    // the maximum commutes with it, and p = 2^((s - m) * scale * log2 e) takes one
-    // FMA and one exp2 per slot. Tiles wholly at or before the wavefront's first
-    // position need no causal mask (wave-uniform).
+  };
+  // Online softmax of this lane's query over tile j's 64 slots (32 here, 32 in
+  // lane ^ 32), in the units of the raw scores q . k: the scale is positive, so
+  // the maximum commutes with it, and p = 2^((s - m) * scale * log2 e) takes one
+  // FMA and one exp2 per slot. Tiles wholly at or before the wavefront's first
+  // position need no causal mask (wave-uniform). The output is rescaled here; the
+  // probabilities leave as the bf16 B operands of the four 16-slot p . v steps.
+  auto softmax = [&](int j, f32x16_pf (&st)[2], u32x4 (&pb)[4]) {
     if ((int64_t)j * kPfSlots + kPfSlots - 1 > (int64_t)a.pos0 + tw) {
       // slots of the tile this lane's query sees: those at most lim past the tile's first
       const int lim = (int)min((int64_t)kPfSlots, max((int64_t)-1, qpos - (int64_t)j * kPfSlots));
@@ -235,24 +234,60 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
-    // O^T += V^T P^T over the four 16-slot steps of the tile.
 #pragma unroll
     for (int js = 0; js < 4; ++js) {
       const f32x16_pf& pt = st[js / 2];
-      uint32_t pk[4];
+      const int r0 = 8 * (js % 2);
+      pb[js] = u32x4{pack2_bf16(pt[r0], pt[r0 + 1]), pack2_bf16(pt[r0 + 2], pt[r0 + 3]),
+                     pack2_bf16(pt[r0 + 4], pt[r0 + 5]), pack2_bf16(pt[r0 + 6], pt[r0 + 7])};
+    }
+  };
+  // O^T += V^T P^T over the four 16-slot steps of the V tile in LDS buffer b.
+  auto pv = [&](int b, const u32x4 (&pb)[4]) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pk[e] = pack2_bf16(pt[8 * (js % 2) + 2 * e], pt[8 * (js % 2) + 2 * e + 1]);
-      const bf16x8_pf pb = __builtin_bit_cast(bf16x8_pf, u32x4{pk[0], pk[1], pk[2], pk[3]});
-      const uint16_t* vr0 = &Vs[buf][col * kPfVRow + 16 * js + 8 * half];
+    for (int js = 0; js < 4; ++js) {
+      const uint16_t* vr0 = &Vs[b][col * kPfVRow + 16 * js + 8 * half];
 #pragma unroll
       for (int dt = 0; dt < kPfD / 32; ++dt) {
         const u32x4 av = *(const u32x4*)(vr0 + 32 * dt * kPfVRow);
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av), pb, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
+                                                        __builtin_bit_cast(bf16x8_pf, pb[js]), o[dt], 0, 0, 0);
       }
     }
-    if (j + 1 < nt) lstore(buf ^ 1);
+  };
+
+  // Wavefronts 4-7 run a phase behind 0-3: in the iteration of tile j they
+  // multiply tile j - 1's p . v first, then tile j's q . k and softmax, so while
+  // the wavefront beside them on their SIMD is in its softmax (VALU) they are in
+  // q . k, and in their softmax it is in p . v (MFMA). V tiles stay for one more
+  // iteration, so the tiles rotate through three LDS buffers. Every output
+  // accumulator takes the same operations in the same order either way.
+  const bool lag = wave >= kPfWaves / 2;  // wave-uniform
+  u32x4 pprev[4];
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  int b = 0;  // LDS buffer of tile j (j mod 3)
+#pragma unroll 1
+  for (int j = 0; j < nt; ++j) {
+    const int bn = b == 2 ? 0 : b + 1;
+    if (j + 1 < nt) gload(j + 1);
+    f32x16_pf st[2];
+    if (!lag) {
+      u32x4 pb[4];
+      qk(b, st);
+      softmax(j, st, pb);
+      pv(b, pb);
+    } else {
+      if (j > 0) pv(b == 0 ? 2 : b - 1, pprev);
+      qk(b, st);
+      softmax(j, st, pprev);
+    }
+    if (j + 1 < nt) lstore(bn);
     __syncthreads();
+    b = bn;
   }
+  if (lag) pv(b == 0 ? 2 : b - 1, pprev);  // tile nt - 1
 
   // out[tq, hq, 32 dt + 8 (r / 4) + 4 half + r % 4] = o / l, four dims per 8-byte store
   if (tq < a.rows) {
