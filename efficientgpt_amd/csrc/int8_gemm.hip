@@ -192,8 +192,8 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
     b_lds[j] = row * kBRow + chunk * 16;
   }
   // Two register staging sets: the loads of step k + 2 are issued while step k is
-  // multiplied and land in LDS at the end of step k + 1, about two steps of MFMA
-  // work later. Loads past the last step re-read the last K slice (in bounds, never
+  // multiplied and land in LDS among the MFMAs of step k + 1, one to two steps of
+  // MFMA work later. Loads past the last step re-read the last K slice (in bounds, never
   // stored), so every load is unconditional and each wait is for one set only.
   const int nk = (SPLIT ? min(a.kchunk, a.K - kbeg) : a.K) / BK;
   u32x4 xr[2][S::kALoads], wr[2][S::kBLoads];
@@ -204,11 +204,14 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
 #pragma unroll
     for (int j = 0; j < S::kBLoads; ++j) wr[set][j] = ld16_stream(wb + (woff[j] + k0));
   };
-  auto store_step = [&](int buf, int set) {
+  // Part q of Q of the LDS stores of one K step (the staging loads j with j % Q == q).
+  auto store_part = [&](int buf, int set, int q, int Q) {
 #pragma unroll
-    for (int j = 0; j < S::kALoads; ++j) *(u32x4*)&As[buf][a_lds[j]] = xr[set][j];
+    for (int j = 0; j < S::kALoads; ++j)
+      if (j % Q == q) *(u32x4*)&As[buf][a_lds[j]] = xr[set][j];
 #pragma unroll
     for (int j = 0; j < S::kBLoads; ++j) {
+      if (j % Q != q) continue;
       if constexpr (BF16B) {
         *(bf16x8*)&Bs16[buf][b_lds[j]] = int8x8_to_bf16(wr[set][j].x, wr[set][j].y);
         *(bf16x8*)&Bs16[buf][b_lds[j] + 8] = int8x8_to_bf16(wr[set][j].z, wr[set][j].w);
@@ -217,6 +220,7 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
       }
     }
   };
+  auto store_step = [&](int buf, int set) { store_part(buf, set, 0, 1); };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -232,8 +236,11 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) b_frag[tn] = (wn0 + tn * 32 + lane % 32) * kBRow + frag_k;
 
-  // The MFMAs of one K step from LDS buffer `buf`, 16 K columns at a time.
-  auto mma_step = [&](int buf) {
+  // The MFMAs of one K step from LDS buffer `buf`, 16 K columns at a time. With
+  // sbuf >= 0 (large tiles) the next step's LDS stores (staging set `set` into
+  // buffer sbuf) are spread over the K sub-steps, after each one's MFMAs, so their
+  // conversions and writes run while the MFMAs do instead of after them.
+  auto mma_step = [&](int buf, int sbuf = -1, int set = 0) {
     if constexpr (TM * TN <= 2) {
       // Small tiles run one wavefront per SIMD with a short MFMA chain per K sub-step, so
       // nothing would cover an LDS read issued just before its MFMA: read every fragment
@@ -288,7 +295,11 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
 #pragma unroll
           for (int tn = 0; tn < TN; ++tn)
             acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bfr[tn], acc[tm][tn], 0, 0, 0);
+        if (sbuf >= 0) store_part(sbuf, set, ks, BK / 16);
       }
+    }
+    if constexpr (TM * TN <= 2) {
+      if (sbuf >= 0) store_step(sbuf, set);
     }
   };
 
@@ -297,26 +308,22 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
   store_step(0, 0);
   __syncthreads();
   // Pairs of steps so the staging sets are fixed registers: step kt computes LDS
-  // buffer kt & 1, refills set kt & 1 with step kt + 2 and stores set (kt + 1) & 1;
-  // an odd last step runs after the loop. Scheduling barriers keep each phase in
+  // buffer kt & 1, refills set kt & 1 with step kt + 2 and stores set (kt + 1) & 1
+  // into the other buffer among its MFMAs; an odd last step runs after the loop. Scheduling barriers keep each phase in
   // place (hoisting the second step's fragment reads above the first step's MFMAs
   // would double the live registers).
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
     load_step(kt + 2, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mma_step(0);
+    mma_step(0, 1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    store_step(1, 1);
     __syncthreads();
     load_step(kt + 3, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mma_step(1);
+    mma_step(1, kt + 2 < nk ? 0 : -1, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 2 < nk) {
-      store_step(0, 0);
-      __syncthreads();
-    }
+    if (kt + 2 < nk) __syncthreads();
   }
   if (kt < nk) mma_step(0);
 
