@@ -466,6 +466,17 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
       return EGPT_LAUNCH_STATUS();
     }
   }
+  if constexpr (BM == 64 && BN == 64 && WN == 2 && NW == 4) {
+    // Fewer tiles than CUs: each block's chain of dependent K steps is the time,
+    // and a 128-wide step halves it (measured on the MI355X: 200 x 2048 -> 2048
+    // 16.5 -> 12.5 us, 160 x 2048 -> 4096 16.8 -> 13.2; with 320 tiles, 300 x 2048
+    // -> 4096, 1.7% slower).
+    if (a.K % kBKSplit == 0 && tiles < 256) {
+      hipLaunchKernelGGL((int8_gemm_kernel<64, 64, kBKSplit, false, 2, 4, false, kBf16B<64, 64>>), dim3(tiles),
+                         dim3(4 * kWave), 0, st, a);
+      return EGPT_LAUNCH_STATUS();
+    }
+  }
   hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false, WN, NW, false, kBf16B<BM, BN>>), dim3(tiles),
                      dim3(NW * kWave), 0, st, a);
   return EGPT_LAUNCH_STATUS();
