@@ -526,10 +526,10 @@ int launch_generic(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw,
   return EGPT_LAUNCH_STATUS();
 }
 
-// K slices for a short-M GEMM whose 64 x 64 tiles leave CUs idle: the fewest
-// (a power of two, at most 16) that give every CU a block, each slice a multiple
-// of kBKSplit and at least 256 wide. 1 when the tiles already fill the chip, or K
-// is short or not a multiple of kBKSplit.
+// K slices for a short-M GEMM (at most 256 rows) whose 64 x 64 tiles leave CUs
+// idle: the fewest (a power of two, at most 16) that give every CU a block, each
+// slice a multiple of kBKSplit and at least 256 wide. 1 when the tiles already fill
+// the chip, or K is short or not a multiple of kBKSplit.
 constexpr int kMinSliceSteps = 4;
 constexpr int kSplitTargetBlocks = 256;
 
@@ -537,7 +537,11 @@ void gemm_split(int64_t M, int64_t N, int64_t K, int& splits, int& kchunk) {
   const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
   splits = 1;
   kchunk = (int)K;
-  if (M > 128 || K % kBKSplit) return;  // taller blocks take the larger tiles below
+  if (M > 256 || K % kBKSplit) return;  // taller blocks take the larger tiles below
+  // Past 128 rows only grids that fill at most half the CUs split (measured on the
+  // MI355X: 200 x 2048 -> 2048, 128 tiles, 12.6 -> 10.1 us with 2 splits; 160 x 2048
+  // -> 4096, 192 tiles, 13.4 -> 16.2 us with 2)
+  if (M > 128 && tiles > kSplitTargetBlocks / 2) return;
   while (tiles * splits < kSplitTargetBlocks && splits < kMaxSplits && K / (2 * splits) >= kMinSliceSteps * kBK) splits *= 2;
   if (splits == 1) return;
   kchunk = (int)(((K + splits - 1) / splits + kBKSplit - 1) / kBKSplit * kBKSplit);

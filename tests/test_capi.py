@@ -117,11 +117,12 @@ def test_struct_layouts_match_the_header(tmp_path):
 
 def test_gemm_split_workspace_policy():
     """Short-M prefill shapes split K until every CU has a block (at most 16 splits, at least 4 K steps of 64
-    each); tall ones and short K do not split."""
+    each); past 128 rows (up to 256) only grids of at most 128 tiles split; tall ones and short K do not split."""
     lib = _lib.lib()
     size = ctypes.c_size_t()
     for (m, n, k), splits in (((128, 2048, 6144), 4), ((128, 4096, 2048), 2), ((64, 2048, 2048), 8),
                               ((17, 64, 12288), 16), ((128, 12288, 2048), 0), ((1024, 2048, 6144), 0),
-                              ((128, 2048, 256), 0)):
+                              ((128, 2048, 256), 0), ((200, 2048, 2048), 2), ((130, 2048, 2048), 4),
+                              ((160, 4096, 2048), 0), ((256, 2048, 6144), 2), ((257, 2048, 2048), 0)):
         assert lib.egpt_int8_gemm_workspace(m, n, k, ctypes.byref(size)) == 0
         assert size.value == splits * m * n * 4, (m, n, k, size.value)
