@@ -146,7 +146,8 @@ template <int BM, int BN, int BK, bool SPLIT, int WN, int NW, bool SWIGLU = fals
 __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8_gemm_kernel(const GemmArgs a) {
   using S = GemmShape<BM, BN, BK, WN, NW>;
   constexpr int TM = S::TM, TN = S::TN;
-  static_assert(!SWIGLU || (!SPLIT && TN % 2 == 0), "the SwiGLU form pairs a wavefront's column tiles");
+  static_assert(!SWIGLU || (!SPLIT && (TN % 2 == 0 || TN == 1)),
+                "the SwiGLU form pairs a wavefront's column tiles, or the two halves of its one tile");
   constexpr int kLdsRow = S::kLdsRow, kLdsRowW = S::kLdsRowW;
   // weight row pitch in LDS: bytes (int8) or bf16 elements (BF16B, the x rows' pitch)
   constexpr int kBRow = BF16B ? kLdsRow : kLdsRowW;
@@ -349,7 +350,31 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
   char* yb = (char*)a.y;
   const int64_t mrow0 = m0 + wm0 + 4 * (lane / 32);
   const uint32_t pitch = (uint32_t)(a.ldy * 2);
-  if constexpr (SWIGLU) {
+  if constexpr (SWIGLU && TN == 1) {
+    // One 32-column tile per wavefront: its columns 0-15 are the gate rows of 16 features and 16-31 their up
+    // rows (swiglu_row), so lane l (column l % 32 < 16) takes u from lane l ^ 16, the same rows one tile half
+    // over. The arithmetic per element is the form below.
+    const int c = lane % 32;
+    const int64_t f = (int64_t)pid_n * (BN / 2) + (wave % WN) * (BN / WN / 2) + (c % 16);
+    const int64_t fc = min(f, (int64_t)a.inter - 1);
+    const float sg_scale = a.scale[fc], su_scale = a.scale[a.inter + fc];
+    const uint32_t base = (uint32_t)((mrow0 * a.ldy + f) * 2);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float up = __shfl_xor(acc[tm][0][r], 16);
+        const int dm = tm * 32 + 8 * (r / 4) + r % 4;
+        if (c < 16 && mrow0 + dm < a.M && f < a.inter) {
+          const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][0][r])) * sg_scale));
+          const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(up)) * su_scale));
+          const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
+          *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(sg * u);
+        }
+      }
+    }
+    return;
+  } else if constexpr (SWIGLU) {
     // act = bf16(bf16(silu(g)) * u) with g and u the product's two roundings (the reference's prefill formula
     // for each), SwiGLU rounded as transformers' bf16 Qwen3MLP (models/qwen3/modeling_qwen3.py:49-62): the same
     // arithmetic per element as the GEMM followed by egpt_silu_mul.
@@ -626,7 +651,21 @@ extern "C" int egpt_int8_gemm_swiglu(const void* x, int64_t ldx, const int8_t* w
                        dim3((unsigned)(a.tiles_m * a.tiles_n)), dim3(kNW256 * kWave), 0, stream, a);
     return EGPT_LAUNCH_STATUS();
   }
-  return EGPT_ERR_UNSUPPORTED;
+  // 64 x 64 tiles (32 features each, gate and up in the two halves of a wavefront's tile) where the plain
+  // product would run them too: not where it would split K, which this form cannot.
+  int splits, kchunk;
+  gemm_split(M, N, K, splits, kchunk);
+  if (splits > 1 || N > INT32_MAX / 2) return EGPT_ERR_UNSUPPORTED;
+  a.tiles_m = (M + 63) / 64;
+  a.tiles_n = (inter + 31) / 32;
+  const unsigned tiles = (unsigned)a.tiles_m * (unsigned)a.tiles_n;
+  if (K % kBKSplit == 0 && tiles < 256)
+    hipLaunchKernelGGL((int8_gemm_kernel<64, 64, kBKSplit, false, 2, 4, true, kBf16B<64, 64>>), dim3(tiles),
+                       dim3(4 * kWave), 0, stream, a);
+  else
+    hipLaunchKernelGGL((int8_gemm_kernel<64, 64, kBK, false, 2, 4, true, kBf16B<64, 64>>), dim3(tiles),
+                       dim3(4 * kWave), 0, stream, a);
+  return EGPT_LAUNCH_STATUS();
 }
 
 extern "C" int egpt_int8_gemm_add_rmsnorm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw,

@@ -107,9 +107,9 @@ int egpt_int8_gemm_ws(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, 
  * (int8 [2 inter, K], scales fp32 [2 inter]); for each row m and feature f, g and u are the product's values of
  * rows f and inter + f (the two roundings above) and act[m, f] = bf16(bf16(silu(g)) * u), transformers' bf16
  * Qwen3MLP rounding (models/qwen3/modeling_qwen3.py:49-62). The same bits as egpt_int8_gemm into a
- * [M, 2 inter] buffer followed by egpt_silu_mul, without that buffer. Only for M > 64 rows and shapes whose large
- * tiles fill the chip (K a multiple of 64, aligned rows, operands under 2 GiB); EGPT_ERR_UNSUPPORTED otherwise,
- * before any launch (the caller runs the two calls). Replaces, with the product, the reference's prefill formula
+ * [M, 2 inter] buffer followed by egpt_silu_mul, without that buffer. For K a multiple of 64, aligned rows and
+ * operands under 2 GiB, and not for shapes whose plain product splits K (egpt_int8_gemm_workspace > 0);
+ * EGPT_ERR_UNSUPPORTED otherwise, before any launch (the caller runs the two calls). Replaces, with the product, the reference's prefill formula
  * for gate_proj / up_proj (research/realmodel/int8_linear.py:96-97) and the SwiGLU its Inductor graph fuses
  * after them. */
 int egpt_int8_gemm_swiglu(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,

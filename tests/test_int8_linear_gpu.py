@@ -405,11 +405,13 @@ def test_gemm_add_rmsnorm_matches_the_two_calls_bit_for_bit(m, k, n):
                                           need.value, st) == _lib.EGPT_ERR_UNSUPPORTED  # 1024 rows: K not split
 
 
-@pytest.mark.parametrize('m,k,inter', [(1024, 2048, 6144), (2048, 4096, 12288), (1100, 512, 7000)])
+@pytest.mark.parametrize('m,k,inter', [(1024, 2048, 6144), (2048, 4096, 12288), (1100, 512, 7000), (128, 2048, 6144),
+                                        (100, 2048, 6144), (200, 2048, 6144), (130, 512, 7000), (40, 4096, 12288)])
 def test_gemm_swiglu_matches_the_two_calls_bit_for_bit(m, k, inter):
     """egpt_int8_gemm_swiglu (SwiGLU in the epilogue of the gate/up product, the gate and up rows of a feature
-    paired in one wavefront) against egpt_int8_gemm into a [m, 2 inter] buffer followed by egpt_silu_mul: the same
-    bits, ragged rows and features included; shapes whose large tiles would not fill the chip are refused."""
+    paired in one wavefront: two column tiles of its large tiles, or the two halves of its one 64 x 64 tile)
+    against egpt_int8_gemm into a [m, 2 inter] buffer followed by egpt_silu_mul: the same bits, ragged rows and
+    features included; a shape whose plain product would split K is refused."""
     from efficientgpt_amd import _lib
     lib = _lib.lib()
     x, q, s = make_case(m, k, 2 * inter, seed=m + inter)
@@ -425,5 +427,6 @@ def test_gemm_swiglu_matches_the_two_calls_bit_for_bit(m, k, inter):
                                      inter, k, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(one, two)
-    assert lib.egpt_int8_gemm_swiglu(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), one.data_ptr(), inter, 100,
-                                     inter, k, st) == _lib.EGPT_ERR_UNSUPPORTED  # 100 rows: the tiles do not fill
+    # 64 rows over 1024 features: the plain product's 32 tiles split K
+    assert lib.egpt_int8_gemm_swiglu(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), one.data_ptr(), inter, 64,
+                                     1024, k, st) == _lib.EGPT_ERR_UNSUPPORTED
