@@ -39,6 +39,9 @@ SIGNATURES = {
                                        _c_vp]),
     'egpt_int8_gemm_add_rmsnorm': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64,
                                             _c_int, _c_int, _c_int, ctypes.c_float, _c_vp, _c_size, _c_vp]),
+    'egpt_int8_gemm_qk_norm_rope': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                             _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _c_int, _c_f, _c_vp, _c_size, _c_vp]),
     'egpt_int8_gemv_splitk_workspace': (_c_int, [_c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)]),
     'egpt_int8_gemv_splitk': (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_int, _c_int, _c_int,
                                        _c_int, _c_vp, _c_size, _c_vp]),

@@ -220,6 +220,22 @@ int gemv_few_rows(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, cons
 int launch_reduce_add_rmsnorm(const float* part, int splits, const float* scale, void* resid, int64_t ld_resid,
                               const void* norm_w, void* y, int64_t ldy, int M, int N, float eps, hipStream_t st);
 
+// The split-K prefill GEMM's partials of the fused QKV product ([splits][rows][(Hq + 2 Hkv) D], fp32) added in
+// split order and rounded as int8_gemm_reduce_kernel does, then egpt_qk_norm_rope's 16-byte form on each
+// (row, head): bit-identical to the reduce launch followed by egpt_qk_norm_rope, with the qkv rows never stored.
+// check_ returns EGPT_OK when the operands take that form (D 32, 64 or 128, 16-byte aligned rows and strides,
+// 2-16 splits), EGPT_ERR_UNSUPPORTED or EGPT_ERR_INVALID otherwise, launching nothing. Defined with the norm
+// kernels (qwen3_step.hip).
+int check_reduce_qk_norm_rope(int splits, const int64_t* positions, const void* q_norm_w, const void* k_norm_w,
+                              const void* cos_t, const void* sin_t, const void* q_out, int64_t ld_q,
+                              const void* k_cache, const void* v_cache, int64_t cache_head_stride,
+                              int64_t cache_slot_stride, int rows, int Hq, int Hkv, int D, int cap);
+int launch_reduce_qk_norm_rope(const float* part, int splits, const float* scale, const int64_t* positions,
+                               const void* q_norm_w, const void* k_norm_w, const void* cos_t, const void* sin_t,
+                               void* q_out, int64_t ld_q, void* k_cache, void* v_cache, int64_t cache_head_stride,
+                               int64_t cache_slot_stride, int rows, int Hq, int Hkv, int D, int cap, float eps,
+                               hipStream_t st);
+
 }  // namespace egpt
 
 // Map a HIP launch result to the library's status convention.

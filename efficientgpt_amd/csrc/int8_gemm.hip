@@ -692,6 +692,37 @@ extern "C" int egpt_int8_gemm_add_rmsnorm(const void* x, int64_t ldx, const int8
                                    eps, stream);
 }
 
+extern "C" int egpt_int8_gemm_qk_norm_rope(const void* x, int64_t ldx, const int8_t* w, int64_t ldw,
+                                           const float* scale, const int64_t* positions, const void* q_norm_w,
+                                           const void* k_norm_w, const void* cos_t, const void* sin_t, void* q_out,
+                                           int64_t ld_q, void* k_cache, void* v_cache, int64_t cache_head_stride,
+                                           int64_t cache_slot_stride, int M, int Hq, int Hkv, int D, int K, int cap,
+                                           float eps, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!x || !w || !scale || M < 0 || K < 0 || Hq < 1 || Hkv < 1 || D < 1) return EGPT_ERR_INVALID;
+  const int64_t N = (int64_t)(Hq + 2 * Hkv) * D;
+  if (ldx < K || ldw < K || N > INT32_MAX) return EGPT_ERR_INVALID;
+  if (M == 0) return EGPT_OK;
+  if (K == 0 || K % kBK || ldx % 8 || ldw % 16 || (uintptr_t)x % 16 || (uintptr_t)w % 16)
+    return EGPT_ERR_UNSUPPORTED;
+  if ((int64_t)M * ldx * 2 >= ((int64_t)1 << 31) || N * ldw >= ((int64_t)1 << 31)) return EGPT_ERR_UNSUPPORTED;
+  int splits, kchunk;
+  gemm_split(M, N, K, splits, kchunk);
+  if (splits < 2) return EGPT_ERR_UNSUPPORTED;  // nothing to fold: egpt_int8_gemm_ws, then egpt_qk_norm_rope
+  const int c = check_reduce_qk_norm_rope(splits, positions, q_norm_w, k_norm_w, cos_t, sin_t, q_out, ld_q, k_cache,
+                                          v_cache, cache_head_stride, cache_slot_stride, M, Hq, Hkv, D, cap);
+  if (c != EGPT_OK) return c;
+  if (!workspace || workspace_bytes < (size_t)splits * (size_t)M * (size_t)N * sizeof(float) ||
+      (uintptr_t)workspace % 16)
+    return EGPT_ERR_WORKSPACE;
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, nullptr, N, M, (int)N, K, 0, 0, splits, kchunk,
+             (float*)workspace};
+  const int st = launch_split_partials(a, stream);
+  if (st != EGPT_OK) return st;
+  return launch_reduce_qk_norm_rope((const float*)workspace, splits, scale, positions, q_norm_w, k_norm_w, cos_t,
+                                    sin_t, q_out, ld_q, k_cache, v_cache, cache_head_stride, cache_slot_stride, M, Hq,
+                                    Hkv, D, cap, eps, stream);
+}
+
 extern "C" int egpt_int8_gemm(const void* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* scale, void* y,
                               int64_t ldy, int M, int N, int K, hipStream_t stream) {
   return egpt_int8_gemm_ws(x, ldx, w, ldw, scale, y, ldy, M, N, K, nullptr, 0, stream);

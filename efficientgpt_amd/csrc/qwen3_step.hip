@@ -190,25 +190,65 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 // and 16-byte accesses (the wavefront-per-head form issues 2-byte accesses). Query and key heads take the decode
 // step's head_norm_rope (the same per-element roundings and the same lane layout and sum order as the step's
 // attention kernel), value heads a 16-byte copy. Groups past the last job compute the last one and store nothing.
+// The q/k/v operands of one launch of the 16-byte form.
+struct QkRope {
+  const int64_t* positions;
+  const uint16_t* qn_w;
+  const uint16_t* kn_w;
+  const uint16_t* cos_t;
+  const uint16_t* sin_t;
+  uint16_t* q_out;
+  int64_t ld_q;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t c_sh, c_sn;
+  int rows, Hq, Hkv, cap;
+  float eps;
+};
+
+// The (row, head) job of this lane group and the lane's first element.
+struct QkJob {
+  int64_t row;
+  int head;
+  int d0;
+  bool store;
+};
+
 template <int D>
-__global__ __launch_bounds__(256) void qk_norm_rope_v8_kernel(
-    const uint16_t* __restrict__ qkv, int64_t ld_qkv, const int64_t* __restrict__ positions,
-    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, const uint16_t* __restrict__ cos_t,
-    const uint16_t* __restrict__ sin_t, uint16_t* __restrict__ q_out, int64_t ld_q, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, int64_t c_sh, int64_t c_sn, int rows, int Hq, int Hkv, int cap, float eps) {
-  constexpr int EPL = 8;
-  constexpr int LPS = D / EPL;  // lanes per head: 16 at D 128
-  const int heads = Hq + 2 * Hkv;
-  const int64_t jobs = (int64_t)rows * heads;
+__device__ __forceinline__ QkJob qk_job(const QkRope& a) {
+  constexpr int LPS = D / 8;  // lanes per head: 16 at D 128
+  const int heads = a.Hq + 2 * a.Hkv;
+  const int64_t jobs = (int64_t)a.rows * heads;
   const int64_t job_raw = (int64_t)blockIdx.x * (256 / LPS) + threadIdx.x / LPS;
-  const bool store = job_raw < jobs;
-  const int64_t job = store ? job_raw : jobs - 1;
-  const int64_t row = job / heads;
-  const int head = (int)(job % heads);
-  const int d0 = (threadIdx.x % LPS) * EPL;
-  int64_t pos = positions[row];
-  pos = pos < 0 ? 0 : (pos >= cap ? cap - 1 : pos);
-  const u32x4 xr = ld16(qkv + row * ld_qkv + (int64_t)head * D + d0);
+  QkJob j;
+  j.store = job_raw < jobs;
+  const int64_t job = j.store ? job_raw : jobs - 1;
+  j.row = job / heads;
+  j.head = (int)(job % heads);
+  j.d0 = (threadIdx.x % LPS) * 8;
+  return j;
+}
+
+// The rest of a job once the lane's 8 elements of its head (xr) are in: value heads copy into the cache, query
+// and key heads take head_norm_rope into q_out / the key cache.
+template <int D>
+__device__ __forceinline__ void qk_finish(const QkRope& a, const QkJob& j, const u32x4 xr) {
+  constexpr int EPL = 8;
+  constexpr int LPS = D / EPL;
+  const int64_t row = j.row;
+  const int head = j.head, d0 = j.d0, Hq = a.Hq, Hkv = a.Hkv;
+  const bool store = j.store;
+  const uint16_t* qn_w = a.qn_w;
+  const uint16_t* kn_w = a.kn_w;
+  const uint16_t* cos_t = a.cos_t;
+  const uint16_t* sin_t = a.sin_t;
+  uint16_t* q_out = a.q_out;
+  uint16_t* k_cache = a.k_cache;
+  uint16_t* v_cache = a.v_cache;
+  const int64_t ld_q = a.ld_q, c_sh = a.c_sh, c_sn = a.c_sn;
+  const float eps = a.eps;
+  int64_t pos = a.positions[row];
+  pos = pos < 0 ? 0 : (pos >= a.cap ? a.cap - 1 : pos);
   if (head >= Hq + Hkv) {  // value head: straight copy into the cache (group-uniform)
     if (store) *(u32x4*)(v_cache + (int64_t)(head - Hq - Hkv) * c_sh + pos * c_sn + d0) = xr;
     return;
@@ -224,6 +264,46 @@ __global__ __launch_bounds__(256) void qk_norm_rope_v8_kernel(
   for (int e = 0; e < 4; ++e) pk[e] = (uint32_t)f32_to_bf16(o[2 * e]) | ((uint32_t)f32_to_bf16(o[2 * e + 1]) << 16);
   uint16_t* dst = is_q ? q_out + row * ld_q + (int64_t)head * D : k_cache + (int64_t)(head - Hq) * c_sh + pos * c_sn;
   if (store) *(u32x4*)(dst + d0) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_v8_kernel(const uint16_t* __restrict__ qkv, int64_t ld_qkv,
+                                                              const QkRope a) {
+  const QkJob j = qk_job<D>(a);
+  qk_finish<D>(a, j, ld16(qkv + j.row * ld_qkv + (int64_t)j.head * D + j.d0));
+}
+
+// launch_reduce_qk_norm_rope's kernel: the lane's 8 elements of the qkv row from the S split partials
+// [S][rows][(Hq + 2 Hkv) D] of the prefill GEMM, added and rounded as int8_gemm_reduce_kernel does (every
+// slice's loads issued before the first addition; bf16(bf16(v0 + v1 + ...) * scale)), then qk_norm_rope_v8's job.
+template <int D, int S>
+__global__ __launch_bounds__(256) void reduce_qk_norm_rope_v8_kernel(const float* __restrict__ part,
+                                                                     const float* __restrict__ scale, const QkRope a) {
+  const QkJob j = qk_job<D>(a);
+  const int64_t n = (int64_t)(a.Hq + 2 * a.Hkv) * D;
+  const int64_t mn = (int64_t)a.rows * n;
+  const int64_t col = (int64_t)j.head * D + j.d0;
+  const float* p = part + j.row * n + col;
+  u32x4 v[S][2];
+#pragma unroll
+  for (int sp = 0; sp < S; ++sp) {
+    v[sp][0] = ld16(p + sp * mn);
+    v[sp][1] = ld16(p + sp * mn + 4);
+  }
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    auto part_e = [&](int sp) {
+      const u32x4& q = v[sp][e / 4];
+      const uint32_t w = (e % 4 == 0) ? q.x : (e % 4 == 1) ? q.y : (e % 4 == 2) ? q.z : q.w;
+      return __uint_as_float(w);
+    };
+    float acc = part_e(0);
+#pragma unroll
+    for (int sp = 1; sp < S; ++sp) acc += part_e(sp);
+    o[e] = bf16r(bf16r(acc) * scale[col + e]);
+  }
+  qk_finish<D>(a, j, pack8(o));
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t ld_gu, int inter,
@@ -439,6 +519,56 @@ int launch_reduce_add_rmsnorm(const float* part, int splits, const float* scale,
                                                   ldy, M, N, eps);
 }
 
+namespace {
+
+template <int D, int S>
+int launch_rqk(int splits, dim3 grid, hipStream_t st, const float* part, const float* scale, const QkRope& a) {
+  if constexpr (S < 2) {
+    return EGPT_ERR_UNSUPPORTED;
+  } else {
+    if (splits != S) return launch_rqk<D, S - 1>(splits, grid, st, part, scale, a);
+    hipLaunchKernelGGL((reduce_qk_norm_rope_v8_kernel<D, S>), grid, dim3(256), 0, st, part, scale, a);
+    return EGPT_LAUNCH_STATUS();
+  }
+}
+
+}  // namespace
+
+int check_reduce_qk_norm_rope(int splits, const int64_t* positions, const void* q_norm_w, const void* k_norm_w,
+                              const void* cos_t, const void* sin_t, const void* q_out, int64_t ld_q,
+                              const void* k_cache, const void* v_cache, int64_t cache_head_stride,
+                              int64_t cache_slot_stride, int rows, int Hq, int Hkv, int D, int cap) {
+  if (!positions || !q_norm_w || !k_norm_w || !cos_t || !sin_t || !q_out || !k_cache || !v_cache)
+    return EGPT_ERR_INVALID;
+  if (rows < 1 || Hq < 1 || Hkv < 1 || cap < 1 || ld_q < (int64_t)Hq * D) return EGPT_ERR_INVALID;
+  if (splits < 2 || splits > kReduceNormMaxSplits || (D != 128 && D != 64 && D != 32)) return EGPT_ERR_UNSUPPORTED;
+  if (ld_q % 8 || cache_head_stride % 8 || cache_slot_stride % 8 || !aligned16p(q_out) || !aligned16p(k_cache) ||
+      !aligned16p(v_cache) || !aligned16p(q_norm_w) || !aligned16p(k_norm_w) || !aligned16p(cos_t) ||
+      !aligned16p(sin_t))
+    return EGPT_ERR_UNSUPPORTED;
+  return EGPT_OK;
+}
+
+int launch_reduce_qk_norm_rope(const float* part, int splits, const float* scale, const int64_t* positions,
+                               const void* q_norm_w, const void* k_norm_w, const void* cos_t, const void* sin_t,
+                               void* q_out, int64_t ld_q, void* k_cache, void* v_cache, int64_t cache_head_stride,
+                               int64_t cache_slot_stride, int rows, int Hq, int Hkv, int D, int cap, float eps,
+                               hipStream_t st) {
+  const int c = check_reduce_qk_norm_rope(splits, positions, q_norm_w, k_norm_w, cos_t, sin_t, q_out, ld_q, k_cache,
+                                          v_cache, cache_head_stride, cache_slot_stride, rows, Hq, Hkv, D, cap);
+  if (c != EGPT_OK) return c;
+  if (!part || !scale || (uintptr_t)part % 16) return EGPT_ERR_INVALID;
+  const QkRope a{positions, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,
+                 (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                 cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps};
+  const int64_t jobs = (int64_t)rows * (Hq + 2 * Hkv);
+  const int per_block = 256 / (D / 8);
+  const dim3 grid((unsigned)((jobs + per_block - 1) / per_block));
+  if (D == 128) return launch_rqk<128, kReduceNormMaxSplits>(splits, grid, st, part, scale, a);
+  if (D == 64) return launch_rqk<64, kReduceNormMaxSplits>(splits, grid, st, part, scale, a);
+  return launch_rqk<32, kReduceNormMaxSplits>(splits, grid, st, part, scale, a);
+}
+
 }  // namespace egpt
 
 using namespace egpt;
@@ -481,11 +611,11 @@ extern "C" int egpt_qk_norm_rope(const void* qkv, int64_t ld_qkv, const int64_t*
   if (v8 && (D == 128 || D == 64 || D == 32)) {
     const int per_block = 256 / (D / 8);  // (row, head) jobs per block
     const dim3 g8((unsigned)((jobs + per_block - 1) / per_block));
-#define EGPT_QKV8(DD)                                                                                                \
-  hipLaunchKernelGGL((qk_norm_rope_v8_kernel<DD>), g8, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, positions, \
-                     (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,                    \
-                     (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,          \
-                     cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps)
+    const QkRope qa{positions, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, (const uint16_t*)cos_t,
+                    (const uint16_t*)sin_t, (uint16_t*)q_out, ld_q, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                    cache_head_stride, cache_slot_stride, rows, Hq, Hkv, cap, eps};
+#define EGPT_QKV8(DD) \
+  hipLaunchKernelGGL((qk_norm_rope_v8_kernel<DD>), g8, dim3(256), 0, stream, (const uint16_t*)qkv, ld_qkv, qa)
     if (D == 128) EGPT_QKV8(128);
     else if (D == 64) EGPT_QKV8(64);
     else EGPT_QKV8(32);

@@ -210,9 +210,10 @@ class Qwen3Int8Engine:
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
 
         # Prompt passes fold the residual add + RMSNorm after o_proj and down_proj into the split-K GEMM's reduce
-        # (egpt_int8_gemm_add_rmsnorm), the next layer's input norm into the down projection and SwiGLU into the
-        # gate/up GEMM (egpt_int8_gemm_swiglu); False runs the separate linear, egpt_add_rmsnorm and egpt_silu_mul
-        # calls instead (the same bits).
+        # (egpt_int8_gemm_add_rmsnorm), q/k norm + RoPE into the split-K QKV reduce (egpt_int8_gemm_qk_norm_rope),
+        # the next layer's input norm into the down projection and SwiGLU into the gate/up GEMM
+        # (egpt_int8_gemm_swiglu); False runs the separate linear, egpt_add_rmsnorm, egpt_qk_norm_rope and
+        # egpt_silu_mul calls instead (the same bits).
         self.fold_norms = True
         pk = weights if packed else pack_qwen3(c, weights)
         check_packed(c, pk)
@@ -451,12 +452,24 @@ class Qwen3Int8Engine:
             _lib.check('egpt_add_rmsnorm', lib.egpt_add_rmsnorm(
                 x.data_ptr(), x.stride(0), down.data_ptr(), down.stride(0), L['in_w'].data_ptr(), h.data_ptr(),
                 h.stride(0), rows, c.hidden, c.rms_eps, st))
-        self._linear(h, L['qkv_q'], L['qkv_s'], qkv, rows, ws)
         kc, vc = self.k_cache[i], self.v_cache[i]
-        _lib.check('egpt_qk_norm_rope', lib.egpt_qk_norm_rope(
-            qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), L['qn_w'].data_ptr(), L['kn_w'].data_ptr(),
-            self.cos.data_ptr(), self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(),
-            kc.stride(0), kc.stride(1), rows, c.heads, c.kv_heads, d, self.cap, c.rms_eps, st))
+        fused = _lib.EGPT_ERR_UNSUPPORTED
+        if rows > MAX_DECODE_ROWS and self.fold_norms and ws is not None:
+            # split-K QKV: the reduce, q/k norm, RoPE and cache write in one launch after the split slices
+            fused = lib.egpt_int8_gemm_qk_norm_rope(
+                h.data_ptr(), h.stride(0), L['qkv_q'].data_ptr(), L['qkv_q'].stride(0), L['qkv_s'].data_ptr(),
+                positions.data_ptr(), L['qn_w'].data_ptr(), L['kn_w'].data_ptr(), self.cos.data_ptr(),
+                self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(), kc.stride(0),
+                kc.stride(1), rows, c.heads, c.kv_heads, d, c.hidden, self.cap, c.rms_eps, ws.data_ptr(), ws.numel(),
+                st)
+        if fused == _lib.EGPT_ERR_UNSUPPORTED:
+            self._linear(h, L['qkv_q'], L['qkv_s'], qkv, rows, ws)
+            _lib.check('egpt_qk_norm_rope', lib.egpt_qk_norm_rope(
+                qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), L['qn_w'].data_ptr(), L['kn_w'].data_ptr(),
+                self.cos.data_ptr(), self.sin.data_ptr(), qrot.data_ptr(), qrot.stride(0), kc.data_ptr(),
+                vc.data_ptr(), kc.stride(0), kc.stride(1), rows, c.heads, c.kv_heads, d, self.cap, c.rms_eps, st))
+        else:
+            _lib.check('egpt_int8_gemm_qk_norm_rope', fused)
         if use_prompt_kernel(rows, pos0):
             _lib.check('egpt_prefill_attn', lib.egpt_prefill_attn(
                 qrot.data_ptr(), qrot.stride(0), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),

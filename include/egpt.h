@@ -127,6 +127,21 @@ int egpt_int8_gemm_add_rmsnorm(const void *x, int64_t ldx, const int8_t *w, int6
                                void *resid, int64_t ld_resid, const void *norm_w, void *y, int64_t ldy,
                                int M, int N, int K, float eps, void *workspace, size_t workspace_bytes,
                                hipStream_t stream);
+/* The split-K product of the fused QKV weights (w [(Hq + 2 Hkv) D, K]) followed by egpt_qk_norm_rope on its rows,
+ * the pair at the start of a prompt pass's attention (transformers' Qwen3Attention.forward, the projections then
+ * q_norm / k_norm, RoPE and the cache update, models/qwen3/modeling_qwen3.py:252-263): the splits' sum and both
+ * roundings of each qkv element, then its head's norm, rotation and store, in one launch after the split slices;
+ * bit-identical to egpt_int8_gemm_ws into a qkv buffer followed by egpt_qk_norm_rope, and the qkv rows themselves
+ * are not stored. Only for shapes that split K (egpt_int8_gemm_workspace(M, (Hq + 2 Hkv) D, K) > 0, the same
+ * workspace), D in {32, 64, 128} and 16-byte aligned rows and strides; EGPT_ERR_UNSUPPORTED otherwise, before any
+ * launch (the caller runs the two calls). Replaces, with egpt_int8_gemm_ws, the reference's prefill formula for
+ * q_proj / k_proj / v_proj (research/realmodel/int8_linear.py:96-97) and what its Inductor graph fuses after it. */
+int egpt_int8_gemm_qk_norm_rope(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                                const int64_t *positions, const void *q_norm_w, const void *k_norm_w,
+                                const void *cos_t, const void *sin_t, void *q_out, int64_t ld_q, void *k_cache,
+                                void *v_cache, int64_t cache_head_stride, int64_t cache_slot_stride, int M, int Hq,
+                                int Hkv, int D, int K, int cap, float eps, void *workspace, size_t workspace_bytes,
+                                hipStream_t stream);
 
 /*
  * Split-K GQA decode attention (flash decoding) with its partial-softmax reduce.

@@ -12,6 +12,8 @@ the output. So the forms agree bit for bit on 99% of the elements and to two ulp
 all, and both match an fp64 restatement of the formula to three.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -149,3 +151,64 @@ def test_qk_norm_rope_vector_and_scalar_forms_agree(d, hq, hkv, rows):
             assert np.all(dd <= 3 * unit), float((dd / unit).max())
         dvs = np.abs(got.double().numpy() - other.double().numpy())
         assert np.all(dvs <= 2 * unit) and np.mean(dvs == 0) >= 0.99
+
+
+@pytest.mark.parametrize('d,hq,hkv,rows,k', [(128, 16, 8, 128, 2048), (128, 32, 8, 40, 4096), (128, 8, 4, 200, 2048),
+                                             (64, 4, 2, 64, 1024), (32, 4, 2, 17, 2048)])
+def test_gemm_qk_norm_rope_matches_the_two_calls_bit_for_bit(d, hq, hkv, rows, k):
+    """egpt_int8_gemm_qk_norm_rope (the split-K QKV product whose reduce also runs q/k norm, RoPE and the cache
+    writes) against egpt_int8_gemm_ws into a qkv buffer followed by egpt_qk_norm_rope: rotated queries, key and
+    value caches the same bits; the rows it does not write stay as they were. A shape whose product does not split
+    K, and a short workspace, are refused before any launch."""
+    lib = _lib.lib()
+    g = torch.Generator().manual_seed(d + hq + rows + k)
+    n = (hq + 2 * hkv) * d
+    cap, pos0 = rows + 40, 25
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).cuda()
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).cuda()
+    s = (torch.rand(n, generator=g) * 0.02 + 1e-3).cuda()
+    qn = (1 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16).cuda()
+    kn = (1 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16).cuda()
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float) / d))
+    ang = torch.arange(cap, dtype=torch.float)[:, None] * inv_freq[None, :]
+    emb = torch.cat([ang, ang], 1)
+    cos, sin = emb.cos().to(torch.bfloat16).cuda(), emb.sin().to(torch.bfloat16).cuda()
+    positions = torch.arange(pos0, pos0 + rows, dtype=torch.long).cuda()
+    need = ctypes.c_size_t()
+    assert lib.egpt_int8_gemm_workspace(rows, n, k, ctypes.byref(need)) == 0
+    assert need.value > 0, 'the case must split K'
+    ws = torch.empty(need.value, dtype=torch.uint8, device='cuda')
+    st = _lib.stream_ptr()
+    out = []
+    for fused in (True, False):
+        q = torch.full((rows, hq * d), float('nan'), dtype=torch.bfloat16, device='cuda')
+        kc = torch.full((hkv, cap, d), 7.0, dtype=torch.bfloat16, device='cuda')
+        vc = torch.full_like(kc, -7.0)
+        if fused:
+            assert lib.egpt_int8_gemm_qk_norm_rope(
+                x.data_ptr(), k, w.data_ptr(), k, s.data_ptr(), positions.data_ptr(), qn.data_ptr(), kn.data_ptr(),
+                cos.data_ptr(), sin.data_ptr(), q.data_ptr(), hq * d, kc.data_ptr(), vc.data_ptr(), kc.stride(0),
+                kc.stride(1), rows, hq, hkv, d, k, cap, 1e-6, ws.data_ptr(), ws.numel(), st) == 0
+        else:
+            qkv = torch.empty(rows, n, dtype=torch.bfloat16, device='cuda')
+            assert lib.egpt_int8_gemm_ws(x.data_ptr(), k, w.data_ptr(), k, s.data_ptr(), qkv.data_ptr(), n, rows, n,
+                                         k, ws.data_ptr(), ws.numel(), st) == 0
+            assert lib.egpt_qk_norm_rope(qkv.data_ptr(), n, positions.data_ptr(), qn.data_ptr(), kn.data_ptr(),
+                                         cos.data_ptr(), sin.data_ptr(), q.data_ptr(), hq * d, kc.data_ptr(),
+                                         vc.data_ptr(), kc.stride(0), kc.stride(1), rows, hq, hkv, d, cap, 1e-6,
+                                         st) == 0
+        torch.cuda.synchronize()
+        out.append((q.cpu(), kc.cpu(), vc.cpu()))
+    (qa, ka, va), (qb, kb, vb) = out
+    assert torch.equal(qa, qb) and not bool(torch.isnan(qa.float()).any())
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    assert bool((ka[:, :pos0] == 7).all()) and bool((va[:, pos0 + rows:] == -7).all())
+    args = (positions.data_ptr(), qn.data_ptr(), kn.data_ptr(), cos.data_ptr(), sin.data_ptr(), q.data_ptr(), hq * d,
+            kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1))
+    assert lib.egpt_int8_gemm_qk_norm_rope(x.data_ptr(), k, w.data_ptr(), k, s.data_ptr(), *args, rows, hq, hkv, d,
+                                           k, cap, 1e-6, ws.data_ptr(), need.value - 4,
+                                           st) == _lib.EGPT_ERR_WORKSPACE
+    # 1024 rows: the product's tiles fill the chip, K is not split
+    assert lib.egpt_int8_gemm_qk_norm_rope(x.data_ptr(), k, w.data_ptr(), k, s.data_ptr(), *args, 1024, hq, hkv, d,
+                                           k, cap, 1e-6, ws.data_ptr(), ws.numel(),
+                                           st) == _lib.EGPT_ERR_UNSUPPORTED
