@@ -263,7 +263,8 @@ def test_small_batch_lds_kernel_four_groups_long_rows():
 
 PREFILL_SHAPES = [(17, 64, 64), (33, 2048, 4096), (128, 2048, 4096), (100, 2048, 6144), (300, 6144, 2048),
                   (1000, 1024, 96), (257, 4096, 1000), (4096, 2048, 2048), (300, 192, 4096), (4096, 128, 4096),
-                  (2100, 704, 4000), (2304, 320, 7424), (1000, 448, 4100), (1024, 512, 2048), (1000, 320, 2100)]
+                  (2100, 704, 4000), (2304, 320, 7424), (1000, 448, 4100), (1024, 512, 2048), (1000, 320, 2100),
+                  (200, 2048, 2048), (130, 2048, 2100), (250, 6144, 2048)]
 
 
 @pytest.mark.parametrize('m,k,n', PREFILL_SHAPES)
@@ -273,7 +274,9 @@ def test_prefill_gemm_kernel_matches_oracle(m, k, n):
     K = 192 an odd number of 64-wide K steps; 4096 x 2048 -> 2048 and 2100 x 704 -> 4000 (ragged) take the
     128 x 256 tile, 4096 x 128 -> 4096 and 2304 x 320 -> 7424 (ragged N, 5 K steps) the 8-wavefront 256 x 256 tile,
     1000 x 448 -> 4100 the 8-wavefront 128 x 128 tile, 1024 x 512 -> 2048 and 1000 x 320 -> 2100 (ragged) the
-    128 x 64 tile; every tile with two wavefronts along M takes its weights into LDS as bf16."""
+    128 x 64 tile; every tile with two wavefronts along M takes its weights into LDS as bf16. 200 x 2048 -> 2048,
+    130 x 2048 -> 2100 (ragged) and 250 x 6144 -> 2048 are 64 x 64 grids with fewer tiles than CUs, which take
+    128-wide K steps."""
     from efficientgpt_amd import _lib
     x, q, s = make_case(m, k, n, seed=m + k + n)
     xd, qd, sd = x.cuda(), q.cuda(), s.cuda()
@@ -288,13 +291,14 @@ def test_prefill_gemm_kernel_matches_oracle(m, k, n):
 
 
 SPLIT_SHAPES = [(128, 6144, 2048), (128, 2048, 4096), (33, 6144, 2048), (64, 2048, 2048), (100, 4096, 1000),
-                (17, 12288, 64)]
+                (17, 12288, 64), (200, 2048, 2048), (130, 2048, 2000), (256, 2048, 2048)]
 
 
 @pytest.mark.parametrize('m,k,n', SPLIT_SHAPES)
 def test_prefill_gemm_split_k_matches_oracle(m, k, n):
-    """Short-M shapes whose 64 x 64 tiles leave CUs idle split K through a workspace (egpt_int8_gemm_ws): the
-    splits' fp32 tiles are added in order, then rounded as the reference's formula. Same bounds as the one-pass
+    """Short-M shapes whose 64 x 64 tiles leave CUs idle split K through a workspace (egpt_int8_gemm_ws; past 128
+    rows, up to 256, grids of at most 128 tiles): the splits' fp32 tiles are added in order, then rounded as the
+    reference's formula. Same bounds as the one-pass
     kernel, and the same result as it on all but the elements whose fp32 sum rounds differently."""
     from efficientgpt_amd import _lib
     import ctypes
