@@ -67,6 +67,13 @@ struct PrefillArgs {
 // Position of slot s (0..15 of a 16-slot step) in the staged V^T row: bits 2 and 3 swapped.
 __device__ __forceinline__ int vperm(int s) { return (s & 3) | ((s >> 2 & 1) << 3) | ((s >> 3 & 1) << 2); }
 
+// The 8-slot (16-byte) chunks of V^T row r sit at chunk index c ^ vswz(r): bit 0 of vswz is row bit 6, bit 1 row
+// bit 5, bit 2 the parity of row bits 2-4. Unswizzled rows are 36 banks apart, so the 16 lanes of an 8-byte
+// store pass (rows 8 apart, one per chunk of dims) all hit the same banks; with it they pair up two to a bank.
+// A 16-byte read pass serves the lanes {0-3, 12-15, 20-23, 24-27} (or {4-7, 8-11, 16-19, 28-31}) of a half
+// wavefront over 64 banks; the p . v reads of those 16 rows (one chunk each) still fall on distinct banks.
+__device__ __forceinline__ int vswz(int r) { return ((r >> 6) & 1) | ((r >> 4) & 2) | ((((r >> 2) ^ (r >> 3) ^ (r >> 4)) & 1) << 2); }
+
 // D: head dim (32, 64 or 128), a multiple of the MFMA's 32 output rows.
 template <int D>
 __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const PrefillArgs a) {
@@ -146,7 +153,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
         *(u32x4*)&Ks[buf][(c / kChunks) * kPfKRow + (c % kChunks) * 8] = sr[i];
       }
     } else if (v_stager) {
-      // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions
+      // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions, in chunk order vswz
       const int p0 = (4 * vg) & ~15;
       const int p = p0 + vperm((4 * vg) & 15);
       // dim 2 w + h of the four slots: the 16-bit half h of word w of each row,
@@ -159,7 +166,8 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
       for (int e = 0; e < 8; ++e) {
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
         const int w = e / 2;
-        *(uint2*)&Vs[buf][(vc * 8 + e) * kPfVRow + p] =
+        const int row = vc * 8 + e;
+        *(uint2*)&Vs[buf][row * kPfVRow + (p ^ (vswz(row) * 8))] =
             make_uint2(__builtin_amdgcn_perm(r1[w], r0[w], sel), __builtin_amdgcn_perm(r3[w], r2[w], sel));
       }
     }
@@ -246,10 +254,10 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
   auto pv = [&](int b, const u32x4 (&pb)[4]) {
 #pragma unroll
     for (int js = 0; js < 4; ++js) {
-      const uint16_t* vr0 = &Vs[b][col * kPfVRow + 16 * js + 8 * half];
 #pragma unroll
       for (int dt = 0; dt < kPfD / 32; ++dt) {
-        const u32x4 av = *(const u32x4*)(vr0 + 32 * dt * kPfVRow);
+        const int row = col + 32 * dt;
+        const u32x4 av = *(const u32x4*)&Vs[b][row * kPfVRow + (((2 * js + half) ^ vswz(row)) * 8)];
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
                                                         __builtin_bit_cast(bf16x8_pf, pb[js]), o[dt], 0, 0, 0);
       }
