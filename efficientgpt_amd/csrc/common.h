@@ -107,6 +107,23 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// ---------------------------------------------------------------- loads straight into LDS
+// global_load_lds_dwordx4: lane i of the load writes the 16 bytes it reads to LDS bytes 16 i .. 16 i + 15 from the
+// wave-uniform base in M0 (checked on the MI355X). The loads come from inline assembly, so the compiler neither
+// tracks nor waits for them: the kernel waits itself (EGPT_WAIT_VMCNT counts every vector memory operation of the
+// wavefront in issue order) and then publishes the data to the other wavefronts with a barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+__device__ __forceinline__ void lds_load16(uint32_t lds_base, const void* g) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void lds_load4(uint32_t lds_base, const void* g) {
+  asm volatile("global_load_lds_dword %0, off" : : "v"(g), "{m0}"(lds_base) : "memory");
+}
+// s_waitcnt vmcnt(n) with the other counters left alone.
+#define EGPT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
 // ---------------------------------------------------------------- DPP reductions
 
 template <int CTRL>

@@ -106,9 +106,6 @@ constexpr int kNW256 = 4;
 constexpr int kWN256 = 4;
 constexpr int kNW128 = 8;
 constexpr int kWN128 = 4;
-// Wavefronts of the 256 x 256 tile and its wave grid.
-constexpr int kNW256x256 = 8;
-constexpr int kWN256x256 = 4;
 
 // Blocks per CU the register allocation must allow (launch bounds): two for the
 // 128 x 256 tile.
@@ -135,6 +132,88 @@ __device__ __forceinline__ void gemm_tile(int b, int tiles_m, int tiles_n, int& 
   const int gm = min(tiles_m - first_m, kGroupM);
   pid_m = first_m + (t % group) % gm;
   pid_n = (t % group) / gm;
+}
+
+// The store of a block's accumulators (TM x TN 32 x 32 tiles per wavefront, wavefront tile origin wm0, wn0 in the
+// block tile m0, n0): y = bf16(bf16(acc) * scale), the reference's two roundings, or with SWIGLU the activation
+// of each feature from its gate and up columns.
+template <int BM, int BN, int TM, int TN, int WN, bool SWIGLU>
+__device__ __forceinline__ void gemm_store(const GemmArgs& a, const f32x16 (&acc)[TM][TN], int64_t m0, int64_t n0,
+                                           int wm0, int wn0, int pid_n, int lane, int wave) {
+  // y = bf16(bf16(acc) * scale): the reference's two roundings. Stores address y
+  // by 32-bit byte offsets from the row of this lane's first accumulator (the
+  // host checks that y spans < 2 GiB); row r of a tile is a constant multiple of
+  // the row pitch away.
+  char* yb = (char*)a.y;
+  const int64_t mrow0 = m0 + wm0 + 4 * (lane / 32);
+  const uint32_t pitch = (uint32_t)(a.ldy * 2);
+  if constexpr (SWIGLU && TN == 1) {
+    // One 32-column tile per wavefront: its columns 0-15 are the gate rows of 16 features and 16-31 their up
+    // rows (swiglu_row), so lane l (column l % 32 < 16) takes u from lane l ^ 16, the same rows one tile half
+    // over. The arithmetic per element is the form below.
+    const int c = lane % 32;
+    const int64_t f = (int64_t)pid_n * (BN / 2) + (wave % WN) * (BN / WN / 2) + (c % 16);
+    const int64_t fc = min(f, (int64_t)a.inter - 1);
+    const float sg_scale = a.scale[fc], su_scale = a.scale[a.inter + fc];
+    const uint32_t base = (uint32_t)((mrow0 * a.ldy + f) * 2);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float up = __shfl_xor(acc[tm][0][r], 16);
+        const int dm = tm * 32 + 8 * (r / 4) + r % 4;
+        if (c < 16 && mrow0 + dm < a.M && f < a.inter) {
+          const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][0][r])) * sg_scale));
+          const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(up)) * su_scale));
+          const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
+          *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(sg * u);
+        }
+      }
+    }
+    return;
+  } else if constexpr (SWIGLU) {
+    // act = bf16(bf16(silu(g)) * u) with g and u the product's two roundings (the reference's prefill formula
+    // for each), SwiGLU rounded as transformers' bf16 Qwen3MLP (models/qwen3/modeling_qwen3.py:49-62): the same
+    // arithmetic per element as the GEMM followed by egpt_silu_mul.
+#pragma unroll
+    for (int tn = 0; tn < TN / 2; ++tn) {
+      const int64_t f = (int64_t)pid_n * (BN / 2) + (wave % WN) * (BN / WN / 2) + tn * 32 + lane % 32;
+      const int64_t fc = min(f, (int64_t)a.inter - 1);
+      const float sg_scale = a.scale[fc], su_scale = a.scale[a.inter + fc];
+      const uint32_t base = (uint32_t)((mrow0 * a.ldy + f) * 2);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dm = tm * 32 + 8 * (r / 4) + r % 4;
+          if (mrow0 + dm < a.M && f < a.inter) {
+            const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][tn][r])) * sg_scale));
+            const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][tn + TN / 2][r])) * su_scale));
+            const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
+            *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(sg * u);
+          }
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int64_t n = n0 + wn0 + tn * 32 + lane % 32;
+    const float sc = a.scale[min(n, (int64_t)a.N - 1)];
+    const uint32_t base = (uint32_t)((mrow0 * a.ldy + n) * 2);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dm = tm * 32 + 8 * (r / 4) + r % 4;
+        if (mrow0 + dm < a.M && n < a.N) {
+          const float v = bf16_to_f32(f32_to_bf16(acc[tm][tn][r]));
+          *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(v * sc);
+        }
+      }
+    }
+  }
 }
 
 // BF16B: the weights are converted to bf16 once, by the thread that loaded them,
@@ -343,80 +422,140 @@ __global__ __launch_bounds__(NW * kWave, (kGemmMinBlocks<BM, BN, NW>)) void int8
     }
     return;
   }
-  // y = bf16(bf16(acc) * scale): the reference's two roundings. Stores address y
-  // by 32-bit byte offsets from the row of this lane's first accumulator (the
-  // host checks that y spans < 2 GiB); row r of a tile is a constant multiple of
-  // the row pitch away.
-  char* yb = (char*)a.y;
-  const int64_t mrow0 = m0 + wm0 + 4 * (lane / 32);
-  const uint32_t pitch = (uint32_t)(a.ldy * 2);
-  if constexpr (SWIGLU && TN == 1) {
-    // One 32-column tile per wavefront: its columns 0-15 are the gate rows of 16 features and 16-31 their up
-    // rows (swiglu_row), so lane l (column l % 32 < 16) takes u from lane l ^ 16, the same rows one tile half
-    // over. The arithmetic per element is the form below.
-    const int c = lane % 32;
-    const int64_t f = (int64_t)pid_n * (BN / 2) + (wave % WN) * (BN / WN / 2) + (c % 16);
-    const int64_t fc = min(f, (int64_t)a.inter - 1);
-    const float sg_scale = a.scale[fc], su_scale = a.scale[a.inter + fc];
-    const uint32_t base = (uint32_t)((mrow0 * a.ldy + f) * 2);
+  gemm_store<BM, BN, TM, TN, WN, SWIGLU>(a, acc, m0, n0, wm0, wn0, pid_n, lane, wave);
+}
+
+// The 256 x 256 tile with its operands loaded straight into LDS (global_load_lds_dwordx4), three K steps of 64
+// in flight: the loads of step k + 2 are issued as step k starts, with no staging registers and no LDS stores by
+// the wavefronts, and each step waits only for its own loads. A step's stage holds the x rows as bf16 (128
+// bytes a row) and the weight rows as int8 (64 bytes a row), 48 KiB; every wavefront converts the weight
+// fragments it reads. Rows carry no padding: the 16-byte chunks of x row r sit at chunk c ^ dma_aswz(r) and those
+// of weight row n at c ^ dma_bswz(n), so the 16 lanes that a 16-byte LDS read serves together ({0-3, 12-15,
+// 20-23, 24-27} or {4-7, 8-11, 16-19, 28-31} of a half wavefront, measured on the MI355X) fall on distinct banks.
+// Each 16-byte weight read feeds two MFMAs: the MFMA k index 8 h + e of sub-step u of K pair p stands for the
+// step's column 32 p + 16 h + 8 u + e in both operands (a permutation of the sum's terms within the step).
+constexpr int kDmaBK = 64;
+constexpr int kDmaWaves = 8;
+constexpr int kDmaStages = 3;
+constexpr int kDmaARow = kDmaBK * 2;                          // bytes per x row of a stage
+constexpr int kDmaBRow = kDmaBK;                              // bytes per weight row of a stage
+constexpr int kDmaAStage = 256 * kDmaARow;                    // 32 KiB
+constexpr int kDmaStage = kDmaAStage + 256 * kDmaBRow;        // 48 KiB
+constexpr int kDmaALoads = kDmaAStage / (kDmaWaves * 1024);   // 1 KiB loads per wavefront and step: 4
+constexpr int kDmaBLoads = 256 * kDmaBRow / (kDmaWaves * 1024);  // 2
+
+__device__ __forceinline__ int dma_aswz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int dma_bswz(int n) { return (n >> 2) & 3; }
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(kDmaWaves * kWave, 1) void int8_gemm_dma_kernel(const GemmArgs a) {
+  constexpr int BM = 256, BN = 256, WN = 4, WM = kDmaWaves / WN;
+  constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);  // 4 x 2 tiles of 32 x 32 per wavefront
+  __shared__ __align__(16) char smem[kDmaStages * kDmaStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int wm0 = (wave / WN) * (BM / WM);
+  const int wn0 = (wave % WN) * (BN / WN);
+  int pid_m, pid_n;
+  gemm_tile((int)blockIdx.x, a.tiles_m, a.tiles_n, pid_m, pid_n);
+  const int64_t m0 = (int64_t)pid_m * BM;
+  const int64_t n0 = (int64_t)pid_n * BN;
+
+  // Load q of a wavefront fills 1 KiB block wave * loads + q of its operand's stage: 8 x rows (lane i: row i / 8,
+  // stored chunk i % 8) or 16 weight rows (lane i: row i / 4, stored chunk i % 4). 32-bit byte offsets from the
+  // operands' bases (the host checks that both span < 2 GiB); rows past M or N read the last one.
+  const char* xb = (const char*)a.x;
+  const char* wb = (const char*)a.w;
+  uint32_t xo[kDmaALoads], wo[kDmaBLoads];
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float up = __shfl_xor(acc[tm][0][r], 16);
-        const int dm = tm * 32 + 8 * (r / 4) + r % 4;
-        if (c < 16 && mrow0 + dm < a.M && f < a.inter) {
-          const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][0][r])) * sg_scale));
-          const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(up)) * su_scale));
-          const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
-          *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(sg * u);
-        }
-      }
-    }
-    return;
-  } else if constexpr (SWIGLU) {
-    // act = bf16(bf16(silu(g)) * u) with g and u the product's two roundings (the reference's prefill formula
-    // for each), SwiGLU rounded as transformers' bf16 Qwen3MLP (models/qwen3/modeling_qwen3.py:49-62): the same
-    // arithmetic per element as the GEMM followed by egpt_silu_mul.
-#pragma unroll
-    for (int tn = 0; tn < TN / 2; ++tn) {
-      const int64_t f = (int64_t)pid_n * (BN / 2) + (wave % WN) * (BN / WN / 2) + tn * 32 + lane % 32;
-      const int64_t fc = min(f, (int64_t)a.inter - 1);
-      const float sg_scale = a.scale[fc], su_scale = a.scale[a.inter + fc];
-      const uint32_t base = (uint32_t)((mrow0 * a.ldy + f) * 2);
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dm = tm * 32 + 8 * (r / 4) + r % 4;
-          if (mrow0 + dm < a.M && f < a.inter) {
-            const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][tn][r])) * sg_scale));
-            const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(acc[tm][tn + TN / 2][r])) * su_scale));
-            const float sg = bf16_to_f32(f32_to_bf16(g / (1.0f + expf(-g))));
-            *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(sg * u);
-          }
-        }
-      }
-    }
-    return;
+  for (int q = 0; q < kDmaALoads; ++q) {
+    const int row = (wave * kDmaALoads + q) * 8 + lane / 8;
+    const int c = (lane % 8) ^ dma_aswz(row);
+    xo[q] = (uint32_t)((min(m0 + row, (int64_t)a.M - 1) * a.ldx + 8 * c) * 2);
   }
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    const int64_t n = n0 + wn0 + tn * 32 + lane % 32;
-    const float sc = a.scale[min(n, (int64_t)a.N - 1)];
-    const uint32_t base = (uint32_t)((mrow0 * a.ldy + n) * 2);
+  for (int q = 0; q < kDmaBLoads; ++q) {
+    const int row = (wave * kDmaBLoads + q) * 16 + lane / 4;
+    const int c = (lane % 4) ^ dma_bswz(row);
+    const int64_t wrow = SWIGLU ? swiglu_row<BN, WN>(pid_n, row, a.inter) : min(n0 + row, (int64_t)a.N - 1);
+    wo[q] = (uint32_t)(wrow * a.ldw + 16 * c);
+  }
+  const uint32_t sbase = lds_addr(smem);
+  auto issue = [&](int kt, int stage) {
+    const uint32_t k0 = (uint32_t)(kt * kDmaBK);
+    const uint32_t abase = sbase + (uint32_t)(stage * kDmaStage);
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
+    for (int q = 0; q < kDmaALoads; ++q)
+      lds_load16(abase + (uint32_t)((wave * kDmaALoads + q) * 1024), xb + (xo[q] + 2 * k0));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dm = tm * 32 + 8 * (r / 4) + r % 4;
-        if (mrow0 + dm < a.M && n < a.N) {
-          const float v = bf16_to_f32(f32_to_bf16(acc[tm][tn][r]));
-          *(uint16_t*)(yb + (base + (uint32_t)dm * pitch)) = f32_to_bf16(v * sc);
-        }
+    for (int q = 0; q < kDmaBLoads; ++q)
+      lds_load16(abase + (uint32_t)(kDmaAStage + (wave * kDmaBLoads + q) * 1024), wb + (wo[q] + k0));
+  };
+
+  // Fragment reads: the swizzles depend on row bits that the wavefront and tile origins (multiples of 32) leave
+  // alone, so each lane's chunk offsets are fixed.
+  const int r32 = lane % 32, h = lane / 32;
+  const int arow = (wm0 + r32) * kDmaARow;               // + tm * 32 rows
+  const int brow = kDmaAStage + (wn0 + r32) * kDmaBRow;  // + tn * 32 rows
+  int ach[2][2], bch[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    bch[p] = 16 * ((2 * p + h) ^ dma_bswz(r32));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) ach[p][u] = 16 * ((4 * p + 2 * h + u) ^ dma_aswz(r32));
+  }
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = f32x16{};
+
+  auto compute = [&](int stage) {
+    const char* sm = smem + stage * kDmaStage;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      bf16x8 bl[TN][2];
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const u32x4 w16 = *(const u32x4*)(sm + brow + tn * 32 * kDmaBRow + bch[p]);
+        bl[tn][0] = int8x8_to_bf16(w16.x, w16.y);
+        bl[tn][1] = int8x8_to_bf16(w16.z, w16.w);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        bf16x8 af[TM];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) af[tm] = *(const bf16x8*)(sm + arow + tm * 32 * kDmaARow + ach[p][u]);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[tm], bl[tn][u], acc[tm][tn], 0, 0, 0);
       }
     }
+  };
+
+  // Step kt: wait for this wavefront's loads of step kt (those of step kt + 1 may stay in flight), publish them
+  // with the barrier (which also retires every wavefront's reads of step kt - 1's stage), refill that stage with
+  // step kt + 2, multiply step kt.
+  const int nk = a.K / kDmaBK;
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  int stage = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk)
+      EGPT_WAIT_VMCNT(kDmaALoads + kDmaBLoads);
+    else
+      EGPT_WAIT_VMCNT(0);
+    lds_barrier();
+    if (kt + 2 < nk) issue(kt + 2, stage == 0 ? 2 : stage - 1);
+    compute(stage);
+    stage = stage == 2 ? 0 : stage + 1;
   }
+  gemm_store<BM, BN, TM, TN, WN, SWIGLU>(a, acc, m0, n0, wm0, wn0, pid_n, lane, wave);
 }
 
 // Split-K reduce: y[m, n] = bf16(bf16(sum_s part[s][m][n]) * scale[n]), splits added in order. The split
@@ -451,8 +590,7 @@ constexpr int kMaxSplits = 16;
 
 // Tiles whose weights go to LDS as bf16 (converted once per block, int8_gemm_kernel's BF16B).
 template <int BM, int BN>
-constexpr bool kBf16B = (BM == 64 && BN == 64) || (BM == 128 && BN == 64) || (BM == 128 && BN == 128) ||
-                        (BM == 256 && BN == 256);
+constexpr bool kBf16B = (BM == 64 && BN == 64) || (BM == 128 && BN == 64) || (BM == 128 && BN == 128);
 
 // The reduce for a.splits (2 ... S) slices; false for a count outside that range.
 template <int S>
@@ -504,6 +642,16 @@ int launch_gemm(GemmArgs a, hipStream_t st) {
   }
   hipLaunchKernelGGL((int8_gemm_kernel<BM, BN, kBK, false, WN, NW, false, kBf16B<BM, BN>>), dim3(tiles),
                      dim3(NW * kWave), 0, st, a);
+  return EGPT_LAUNCH_STATUS();
+}
+
+// The 256 x 256 LDS-direct tiles (K a multiple of 64); with SWIGLU each block covers 128 features.
+template <bool SWIGLU>
+int launch_gemm_dma(GemmArgs a, hipStream_t st) {
+  a.tiles_m = (int)(((int64_t)a.M + 255) / 256);
+  a.tiles_n = SWIGLU ? (int)(((int64_t)a.inter + 127) / 128) : (int)(((int64_t)a.N + 255) / 256);
+  hipLaunchKernelGGL((int8_gemm_dma_kernel<SWIGLU>), dim3((unsigned)a.tiles_m * (unsigned)a.tiles_n),
+                     dim3(kDmaWaves * kWave), 0, st, a);
   return EGPT_LAUNCH_STATUS();
 }
 
@@ -613,7 +761,7 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
     }
   }
 // The largest tile that still gives every CU a block; small M keeps more, narrower tiles.
-  if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm<256, 256, kWN256x256, kNW256x256>(a, stream);
+  if (M > 128 && gemm_blocks<256, 256>(a) >= 256) return launch_gemm_dma<false>(a, stream);
   if (M > 64 && gemm_blocks<128, 256>(a) >= 256) return launch_gemm<128, 256, kWN256, kNW256>(a, stream);
   if (M > 64 && gemm_blocks<128, 128>(a) >= 256) return launch_gemm<128, 128, kWN128, kNW128>(a, stream);
   if (M > 64 && gemm_blocks<128, 64>(a) >= 256) return launch_gemm<128, 64>(a, stream);
@@ -637,13 +785,7 @@ extern "C" int egpt_int8_gemm_swiglu(const void* x, int64_t ldx, const int8_t* w
   auto blocks = [&](int bm, int bn) {
     return (int64_t)((M + bm - 1) / bm) * ((inter + bn / 2 - 1) / (bn / 2));
   };
-  if (M > 128 && blocks(256, 256) >= 256) {
-    a.tiles_m = (M + 255) / 256;
-    a.tiles_n = (inter + 127) / 128;
-    hipLaunchKernelGGL((int8_gemm_kernel<256, 256, kBK, false, kWN256x256, kNW256x256, true, kBf16B<256, 256>>),
-                       dim3((unsigned)(a.tiles_m * a.tiles_n)), dim3(kNW256x256 * kWave), 0, stream, a);
-    return EGPT_LAUNCH_STATUS();
-  }
+  if (M > 128 && blocks(256, 256) >= 256) return launch_gemm_dma<true>(a, stream);
   if (M > 64 && blocks(128, 256) >= 256) {
     a.tiles_m = (M + 127) / 128;
     a.tiles_n = (inter + 127) / 128;

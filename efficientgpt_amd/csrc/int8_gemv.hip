@@ -406,17 +406,6 @@ __global__ __launch_bounds__(kMfmaWaves * kWave) void gemv_i8_mfma_walk(
 // the compiler, seeing them, waits for all of them before any LDS read.
 constexpr int kLdsChunk = 512;
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
-}
-__device__ __forceinline__ void lds_load16(uint32_t lds_base, const void* g) {
-  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(lds_base) : "memory");
-}
-__device__ __forceinline__ void lds_load4(uint32_t lds_base, const void* g) {
-  asm volatile("global_load_lds_dword %0, off" : : "v"(g), "{m0}"(lds_base) : "memory");
-}
-// s_waitcnt vmcnt(n) with the other counters left alone.
-#define EGPT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
 template <int FG>
 __device__ __forceinline__ void lds_chunk_issue(int8_t* buf, const int8_t* __restrict__ w, int64_t ldw, int N,

@@ -264,7 +264,7 @@ def test_small_batch_lds_kernel_four_groups_long_rows():
 PREFILL_SHAPES = [(17, 64, 64), (33, 2048, 4096), (128, 2048, 4096), (100, 2048, 6144), (300, 6144, 2048),
                   (1000, 1024, 96), (257, 4096, 1000), (4096, 2048, 2048), (300, 192, 4096), (4096, 128, 4096),
                   (2100, 704, 4000), (2304, 320, 7424), (1000, 448, 4100), (1024, 512, 2048), (1000, 320, 2100),
-                  (200, 2048, 2048), (130, 2048, 2100), (250, 6144, 2048)]
+                  (200, 2048, 2048), (130, 2048, 2100), (250, 6144, 2048), (4096, 64, 4096), (4100, 192, 4000)]
 
 
 @pytest.mark.parametrize('m,k,n', PREFILL_SHAPES)
@@ -272,7 +272,8 @@ def test_prefill_gemm_kernel_matches_oracle(m, k, n):
     """More than 16 rows: the MFMA GEMM (egpt_int8_gemm), against the oracle's prefill formula
     bf16(fp32(bf16(x q^T)) s) and the reference's tolerance; odd N and M exercise the masked edges,
     K = 192 an odd number of 64-wide K steps; 4096 x 2048 -> 2048 and 2100 x 704 -> 4000 (ragged) take the
-    128 x 256 tile, 4096 x 128 -> 4096 and 2304 x 320 -> 7424 (ragged N, 5 K steps) the 8-wavefront 256 x 256 tile,
+    128 x 256 tile, 4096 x 128 -> 4096, 2304 x 320 -> 7424 (5 K steps), 4096 x 64 -> 4096 (one K step) and
+    4100 x 192 -> 4000 (ragged M and N) the 256 x 256 tile whose operands go straight into LDS,
     1000 x 448 -> 4100 the 8-wavefront 128 x 128 tile, 1024 x 512 -> 2048 and 1000 x 320 -> 2100 (ragged) the
     128 x 64 tile; every tile with two wavefronts along M takes its weights into LDS as bf16. 200 x 2048 -> 2048,
     130 x 2048 -> 2100 (ragged) and 250 x 6144 -> 2048 are 64 x 64 grids with fewer tiles than CUs, which take
