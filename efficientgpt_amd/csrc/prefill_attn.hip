@@ -15,9 +15,9 @@
 // A block is 8 wavefronts over one kv head; each wavefront owns 32 consecutive
 // query rows of one query head, so a block covers min(group, 4) query heads and
 // 32 * 8 / min(group, 4) positions, and every head of the block shares the K/V
-// tiles it stages. K/V advance 64 slots at a time through three LDS buffers (the
-// global loads of tile j + 1 are issued before tile j is multiplied; wavefronts
-// 4-7 run a phase behind 0-3 and read tile j - 1's V during tile j).
+// tiles it stages. K/V advance 64 slots at a time, loaded straight into LDS
+// (global_load_lds_dwordx4) two tiles ahead, through three K and four V buffers
+// (wavefronts 4-7 run a phase behind 0-3 and read tile j - 1's V during tile j).
 //
 // Per tile and wavefront, with v_mfma_f32_32x32x16_bf16 (lane l holds A[l % 32]
 // [8 (l / 32) + e] and B[8 (l / 32) + e][l % 32]; accumulator register r of lane
@@ -29,9 +29,11 @@
 //   * O^T += V^T P^T: the probabilities go from those accumulators straight into
 //     the B operand (no LDS round trip). That operand's k index 8 (l / 32) + e
 //     then stands for slot 8 (e / 4) + 4 (l / 32) + e % 4 of a 16-slot step
-//     (bits 2 and 3 of the slot swapped), so V^T is staged in LDS with its slots
-//     in that order. The output accumulators also hold one query per lane, so the
-//     online-softmax rescale is per lane too.
+//     (bits 2 and 3 of the slot swapped). V stays slot-major in LDS; the A operand
+//     V^T takes two transposing reads (ds_read_b64_tr_b16) per MFMA, slots
+//     4 (l / 32) + 0..3 and 8 + 4 (l / 32) + 0..3 of the step. The output
+//     accumulators also hold one query per lane, so the online-softmax rescale is
+//     per lane too.
 // Padding query rows (past `rows`) read a valid row and are never stored; slots
 // past the block's last position read the last one and are masked.
 #include "common.h"
@@ -45,8 +47,6 @@ typedef float f32x16_pf __attribute__((ext_vector_type(16)));
 constexpr int kPfSlots = 64;           // K/V slots per tile
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
-constexpr int kPfStage = kPfThreads / 2;  // threads staging K (and as many staging V)
-constexpr int kPfVRow = kPfSlots + 8;  // bf16 per V^T row in LDS
 constexpr float kPfLog2e = 1.4426950408889634f;
 
 struct PrefillArgs {
@@ -64,25 +64,31 @@ struct PrefillArgs {
   float scale;
 };
 
-// Position of slot s (0..15 of a 16-slot step) in the staged V^T row: bits 2 and 3 swapped.
-__device__ __forceinline__ int vperm(int s) { return (s & 3) | ((s >> 2 & 1) << 3) | ((s >> 3 & 1) << 2); }
+typedef short v4i16_pf __attribute__((ext_vector_type(4)));
 
-// The 8-slot (16-byte) chunks of V^T row r sit at chunk index c ^ vswz(r): bit 0 of vswz is row bit 6, bit 1 row
-// bit 5, bit 2 the parity of row bits 2-4. Unswizzled rows are 36 banks apart, so the 16 lanes of an 8-byte
-// store pass (rows 8 apart, one per chunk of dims) all hit the same banks; with it they pair up two to a bank.
-// A 16-byte read pass serves the lanes {0-3, 12-15, 20-23, 24-27} (or {4-7, 8-11, 16-19, 28-31}) of a half
-// wavefront over 64 banks; the p . v reads of those 16 rows (one chunk each) still fall on distinct banks.
-__device__ __forceinline__ int vswz(int r) { return ((r >> 6) & 1) | ((r >> 4) & 2) | ((((r >> 2) ^ (r >> 3) ^ (r >> 4)) & 1) << 2); }
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane l receives element l % 4 of the four
+// 16-bit elements at the addresses of lanes (l % 16) / 4 + 4 i, i = 0..3 (checked on the MI355X).
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) v4i16_pf*)(const void*)p));
+}
 
 // D: head dim (32, 64 or 128), a multiple of the MFMA's 32 output rows.
 template <int D>
 __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const PrefillArgs a) {
   constexpr int kPfD = D;
-  constexpr int kPfKRow = kPfD + 8;     // bf16 per K row in LDS (16 bytes of padding)
-  constexpr int kChunks = kPfD / 8;     // 16-byte chunks per K/V row
-  constexpr int kLoads = kChunks / 4;   // 16-byte loads per staging thread and tile: 64 slots x kChunks / 256
-  __shared__ __align__(16) uint16_t Ks[3][kPfSlots * kPfKRow];
-  __shared__ __align__(16) uint16_t Vs[3][kPfD * kPfVRow];
+  constexpr int kChunks = kPfD / 8;     // 16-byte chunks per K/V row (slot)
+  constexpr int kLogC = kPfD == 128 ? 4 : kPfD == 64 ? 3 : 2;
+  constexpr int kRow = 2 * kPfD;        // bytes per slot row in LDS (no padding: chunks swizzled)
+  constexpr int kTile = kPfSlots * kRow;
+  constexpr int kTileLoads = 2 * kTile / (kPfWaves * 1024);  // 1 KiB LDS-direct loads per wavefront and tile
+  // K row r keeps chunk c at c ^ kswz(r), so the 16 rows a 16-byte read pass serves ({0-3, 12-15, 20-23,
+  // 24-27} or {4-7, 8-11, 16-19, 28-31} of a half wavefront) land on distinct banks; V row r at c ^ vswz(r),
+  // so the four rows x 64 bytes of a transposing read pass do.
+  auto kswz = [](int r) { return (r >> (4 - kLogC)) & (kChunks - 1); };
+  auto vswz = [](int r) { return 4 * ((r & 3) >> (4 - kLogC)); };
+  __shared__ __align__(16) char Ks[3][kTile];
+  __shared__ __align__(16) char Vs[4][kTile];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -106,72 +112,39 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
   const int64_t last = (int64_t)a.pos0 + min(t0 + a.bt, a.rows) - 1;
   const int nt = (int)(last / kPfSlots) + 1;
 
-  // B fragments of Q^T: this lane's query, dims 16 kk + 8 half .. + 7.
+  // Loads of one K/V tile (64 slots x kChunks chunks of 8 dims each, K then V): 1 KiB blocks t = wave + 8 q;
+  // lane i of a block fills row i / kChunks, stored chunk i % kChunks. Slots past the block's last position read
+  // the last one.
+  const uint16_t* kb = a.k + (int64_t)hk * a.c_sh;
+  const uint16_t* vb = a.v + (int64_t)hk * a.c_sh;
+  const uint32_t kbase = lds_addr(&Ks[0][0]), vbase = lds_addr(&Vs[0][0]);
+  auto issue = [&](int j) {
+#pragma unroll
+    for (int q = 0; q < kTileLoads; ++q) {
+      const int t = wave + kPfWaves * q;
+      const bool isk = t < kTile / 1024;  // wave-uniform
+      const int blk = isk ? t : t - kTile / 1024;
+      const int row = blk * (1024 / kRow) + lane / kChunks;
+      const int c = (lane % kChunks) ^ (isk ? kswz(row) : vswz(row));
+      const int64_t sl = min((int64_t)j * kPfSlots + row, last);
+      const uint32_t dst = isk ? kbase + (uint32_t)((j % 3) * kTile + blk * 1024)
+                               : vbase + (uint32_t)((j % 4) * kTile + blk * 1024);
+      lds_load16(dst, (isk ? kb : vb) + sl * a.c_sn + 8 * c);
+    }
+  };
+
+  // B fragments of Q^T: this lane's query, dims 16 kk + 8 half .. + 7, loaded while tile 0 is, and waited for
+  // before the loop: the compiler does not see the LDS-direct loads, so a load of its own still pending in the
+  // loop would make it wait for every load in flight before each q . k.
+  issue(0);
   u32x4 qf[kPfD / 16];
   {
     const uint16_t* qrow = a.q + (int64_t)min(tq, a.rows - 1) * a.q_ld + (int64_t)hq * kPfD + 8 * half;
 #pragma unroll
     for (int kk = 0; kk < kPfD / 16; ++kk) qf[kk] = ld16(qrow + 16 * kk);
   }
-
-  // Staging of one K/V tile: 64 slots x kChunks chunks of 8 dims each for K and V.
-  // The first 4 wavefronts stage V, the other 4 K, so every thread keeps kLoads
-  // 16-byte loads in flight (4 at D 128). A K thread t takes chunks (slot c /
-  // kChunks, chunk c % kChunks) for c = t + 256 i; a V thread t < 64 kChunks / 4
-  // takes chunk vc = t % kChunks of the four consecutive slots 4 vg .. 4 vg + 3 (vg
-  // = t / kChunks), whose staged positions are consecutive too (vperm keeps bits 0
-  // and 1), so each of its 8 dims is one 8-byte LDS store; at D < 128 the other V
-  // threads stage nothing.
-  const uint16_t* kb = a.k + (int64_t)hk * a.c_sh;
-  const uint16_t* vb = a.v + (int64_t)hk * a.c_sh;
-  const int stid = tid % kPfStage;
-  const bool do_k = tid >= kPfStage;  // wave-uniform
-  const int vg = stid / kChunks, vc = stid % kChunks;
-  const bool v_stager = vg < kPfSlots / 4;
-  u32x4 sr[4];
-  auto gload = [&](int j) {
-    if (do_k) {
-#pragma unroll
-      for (int i = 0; i < kLoads; ++i) {
-        const int c = stid + kPfStage * i;
-        const int64_t s = min((int64_t)j * kPfSlots + c / kChunks, last);
-        sr[i] = ld16(kb + s * a.c_sn + (c % kChunks) * 8);
-      }
-    } else if (v_stager) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t s = min((int64_t)j * kPfSlots + 4 * vg + i, last);
-        sr[i] = ld16(vb + s * a.c_sn + vc * 8);
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-    if (do_k) {
-#pragma unroll
-      for (int i = 0; i < kLoads; ++i) {
-        const int c = stid + kPfStage * i;
-        *(u32x4*)&Ks[buf][(c / kChunks) * kPfKRow + (c % kChunks) * 8] = sr[i];
-      }
-    } else if (v_stager) {
-      // V^T: dim vc * 8 + e of slots 4 vg .. 4 vg + 3 at their staged positions, in chunk order vswz
-      const int p0 = (4 * vg) & ~15;
-      const int p = p0 + vperm((4 * vg) & 15);
-      // dim 2 w + h of the four slots: the 16-bit half h of word w of each row,
-      // two slots per v_perm_b32 (bytes 0-1 or 2-3 of each source)
-      const uint32_t r0[4] = {sr[0].x, sr[0].y, sr[0].z, sr[0].w};
-      const uint32_t r1[4] = {sr[1].x, sr[1].y, sr[1].z, sr[1].w};
-      const uint32_t r2[4] = {sr[2].x, sr[2].y, sr[2].z, sr[2].w};
-      const uint32_t r3[4] = {sr[3].x, sr[3].y, sr[3].z, sr[3].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const int w = e / 2;
-        const int row = vc * 8 + e;
-        *(uint2*)&Vs[buf][row * kPfVRow + (p ^ (vswz(row) * 8))] =
-            make_uint2(__builtin_amdgcn_perm(r1[w], r0[w], sel), __builtin_amdgcn_perm(r3[w], r2[w], sel));
-      }
-    }
-  };
+  EGPT_WAIT_VMCNT(0);
+  if (nt > 1) issue(1);
 
   f32x16_pf o[kPfD / 32];
 #pragma unroll
@@ -188,7 +161,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
     for (int kk = 0; kk < kPfD / 16; ++kk)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const u32x4 av = *(const u32x4*)&Ks[b][(32 * mt + col) * kPfKRow + 8 * half + 16 * kk];
+        const u32x4 av = *(const u32x4*)&Ks[b][(32 * mt + col) * kRow + 16 * ((2 * kk + half) ^ kswz(col))];
         st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
                                                          __builtin_bit_cast(bf16x8_pf, qf[kk]), st[mt], 0, 0, 0);
       }
@@ -250,14 +223,22 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
                      pack2_bf16(pt[r0 + 4], pt[r0 + 5]), pack2_bf16(pt[r0 + 6], pt[r0 + 7])};
     }
   };
-  // O^T += V^T P^T over the four 16-slot steps of the V tile in LDS buffer b.
+  // O^T += V^T P^T over the four 16-slot steps of the V tile in LDS buffer b. Lane s points its two transposing
+  // reads at slot 4 (s / 32) + (s % 16) / 4 (and 8 slots on) of the step, dims 32 dt + 16 ((s / 16) % 2) +
+  // 4 (s % 4) .. + 3, so lane l receives V^T[32 dt + l % 32][the step's slots 4 (l / 32) + 0..3, then + 8].
+  const int vrow = 4 * half + (lane % 16) / 4;
+  int voff[kPfD / 32];
+#pragma unroll
+  for (int dt = 0; dt < kPfD / 32; ++dt)
+    voff[dt] = vrow * kRow + 16 * ((4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) ^ vswz(vrow)) + 8 * (lane & 1);
   auto pv = [&](int b, const u32x4 (&pb)[4]) {
 #pragma unroll
     for (int js = 0; js < 4; ++js) {
 #pragma unroll
       for (int dt = 0; dt < kPfD / 32; ++dt) {
-        const int row = col + 32 * dt;
-        const u32x4 av = *(const u32x4*)&Vs[b][row * kPfVRow + (((2 * js + half) ^ vswz(row)) * 8)];
+        const char* vp = &Vs[b][16 * js * kRow + voff[dt]];
+        const uint2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * kRow);
+        const u32x4 av{lo.x, lo.y, hi.x, hi.y};
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_pf, av),
                                                         __builtin_bit_cast(bf16x8_pf, pb[js]), o[dt], 0, 0, 0);
       }
@@ -268,34 +249,35 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
   // multiply tile j - 1's p . v first, then tile j's q . k and softmax, so while
   // the wavefront beside them on their SIMD is in its softmax (VALU) they are in
   // q . k, and in their softmax it is in p . v (MFMA). V tiles stay for one more
-  // iteration, so the tiles rotate through three LDS buffers. Every output
-  // accumulator takes the same operations in the same order either way.
+  // iteration, so V rotates through four LDS buffers and K through three. Every
+  // output accumulator takes the same operations in the same order either way.
   const bool lag = wave >= kPfWaves / 2;  // wave-uniform
   u32x4 pprev[4];
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  int b = 0;  // LDS buffer of tile j (j mod 3)
+  // Tile j: wait for this wavefront's loads of tile j (tile j + 1's stay in flight), publish them with the
+  // barrier, which also retires every wavefront's reads of K tile j - 1 and V tile j - 2, load tile j + 2 into
+  // those buffers, multiply tile j.
 #pragma unroll 1
   for (int j = 0; j < nt; ++j) {
-    const int bn = b == 2 ? 0 : b + 1;
-    if (j + 1 < nt) gload(j + 1);
+    if (j + 1 < nt)
+      EGPT_WAIT_VMCNT(kTileLoads);
+    else
+      EGPT_WAIT_VMCNT(0);
+    lds_barrier();
+    if (j + 2 < nt) issue(j + 2);
+    const int kbuf = j % 3, vbuf = j % 4;
     f32x16_pf st[2];
     if (!lag) {
       u32x4 pb[4];
-      qk(b, st);
+      qk(kbuf, st);
       softmax(j, st, pb);
-      pv(b, pb);
+      pv(vbuf, pb);
     } else {
-      if (j > 0) pv(b == 0 ? 2 : b - 1, pprev);
-      qk(b, st);
+      if (j > 0) pv(vbuf == 0 ? 3 : vbuf - 1, pprev);
+      qk(kbuf, st);
       softmax(j, st, pprev);
     }
-    if (j + 1 < nt) lstore(bn);
-    __syncthreads();
-    b = bn;
   }
-  if (lag) pv(b == 0 ? 2 : b - 1, pprev);  // tile nt - 1
+  if (lag) pv((nt - 1) % 4, pprev);  // tile nt - 1
 
   // out[tq, hq, 32 dt + 8 (r / 4) + 4 half + r % 4] = o / l, four dims per 8-byte store
   if (tq < a.rows) {
