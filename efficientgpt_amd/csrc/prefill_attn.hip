@@ -9,8 +9,10 @@
 // would rescan the prefix once per query row. bf16 q, k, v and output; the logits
 // (q . k) * scale and the online softmax in fp32; the probabilities enter the
 // p . v products as bf16, as in SDPA's bf16 flash path; the softmax runs in the
-// units of the raw scores, p = 2^((q.k - max) * scale * log2 e), the flash form's
-// folded scale.
+// units of the raw scores, p = 2^((q.k - m) * scale * log2 e), the flash form's
+// folded scale, with a reference maximum m that moves only when a tile's maximum
+// passes it by more than 8 in the exponent (so p < 2^8 and the output is rescaled
+// on few tiles).
 //
 // A block is 8 wavefronts over one kv head; each wavefront owns 32 consecutive
 // query rows of one query head, so a block covers min(group, 4) query heads and
@@ -48,6 +50,7 @@ constexpr int kPfSlots = 64;           // K/V slots per tile
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr float kPfLog2e = 1.4426950408889634f;
+constexpr float kPfLazy = 8.f;  // exponent by which a score may pass the softmax's reference maximum (p < 2^8)
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -191,10 +194,15 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
     LanePair pr = pair32(mx);
     mx = fmaxf(pr.lo, pr.hi);
-    const float mn = fmaxf(m, mx);
-    const float mref = mn == -INFINITY ? 0.f : mn;
+    // The reference maximum m moves only when the tile's maximum passes it by more than kPfLazy in the exponent,
+    // so the probabilities stay below 2^kPfLazy (the output is o / l whichever maximum they are taken against)
+    // and the output is rescaled only on those tiles. m starts at -inf: the first tile with a visible slot sets
+    // it (mx - m is then +inf), a tile with none leaves it (NaN or -inf compare false).
     const float c = a.scale * kPfLog2e;
-    const float alpha = __builtin_amdgcn_exp2f((m - mref) * c);
+    const bool move = (mx - m) * c > kPfLazy;
+    const float mn = move ? mx : m;
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = move ? __builtin_amdgcn_exp2f((m - mref) * c) : 1.f;
     const float off = -mref * c;
     float ps = 0.f;
 #pragma unroll
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
     ps = pr.lo + pr.hi;
     l = l * alpha + ps;
     m = mn;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // once the maxima settle alpha is exactly 1
+    if (__builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
       for (int dt = 0; dt < kPfD / 32; ++dt)
 #pragma unroll
