@@ -796,7 +796,8 @@ def main():
     step_bytes = wbytes + sbytes + cfg.kv_bytes_per_slot() * mean_len + 2 * cfg.hidden
     step_s = wall / args.steps
     line = {
-        'metric': 'batch-1 decode tok/s (Qwen3-1.7B-shape int8); GEMV/attn HBM GB/s vs peak',
+        'metric': 'batch-1 decode tok/s (Qwen3-%s-shape int8); GEMV/attn HBM GB/s vs peak'
+                  % ('1.7B' if args.model == 'qwen3-1.7b' else '8B'),
         'value': round(value, 2), 'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
         'ms_per_step': round(step_s * 1e3, 4), 'gpu_ms_per_step': round(gpu_s / args.steps * 1e3, 4),
         'spread': rounds_rec, 'host_cpu': cpu_name(),
