@@ -10,7 +10,8 @@ sums add far less). Each case must meet that bound and the 2e-2 relative bar.
 Query heads per kv head 1, 2, 4 and 8 (and 3 and 6, which take blocks of 1 and 2
 query heads); head dims 128, 64 and 32; prompts that start at slot 0 and ones that
 continue a filled cache; strided rows; NaN in every slot past the block, which must
-leave the output bit-identical; logits scaled x8.
+leave the output bit-identical; logits scaled x8; scores that climb along the prompt
+and jump at a late slot, so the softmax's reference maximum moves many times.
 """
 
 import numpy as np
@@ -87,6 +88,23 @@ def test_prefill_attention_strided_rows_and_scaled_logits(hq, hkv):
     # q rows inside a wider buffer (the rotated queries of the fused QKV rows), output rows wider than the heads
     q, k, v, o_pad = _case(200, hq, hkv, 260, 40, seed=3, scale=8 ** 0.5, q_pad=2 * hkv * D, o_pad=64)
     _check(q, k, v, hq, hkv, 40, o_pad=o_pad)
+
+
+@pytest.mark.parametrize('hq,hkv', [(16, 8), (32, 8)])
+def test_prefill_attention_climbing_scores_and_a_late_spike(hq, hkv):
+    # Non-negative queries against keys whose size climbs 60-fold along the slots: each query's maximum score
+    # passes the softmax's reference maximum by more than 2^8 many times over the prompt; one key far larger
+    # still (slot 700) makes it jump once more by hundreds of exponents, after which the rows attend almost only
+    # to that slot. Every row must stay within the same bound of the fp64 truth.
+    rows, cap = 1000, 1000
+    g = torch.Generator().manual_seed(21)
+    q = (torch.randn(rows, hq * D, generator=g).abs() * 0.5).to(torch.bfloat16)
+    ramp = torch.linspace(0.2, 12.0, cap).view(1, cap, 1)
+    kf = torch.randn(hkv, cap, D, generator=g).abs() * ramp
+    kf[:, 700] = 40.0
+    k = kf.to(torch.bfloat16)
+    v = torch.randn(hkv, cap, D, generator=g).to(torch.bfloat16)
+    _check(q, k, v, hq, hkv, 0)
 
 
 @pytest.mark.parametrize('hq,hkv', [(16, 8), (32, 8)])
