@@ -274,14 +274,22 @@ __global__ __launch_bounds__(kPfThreads, 1) void prefill_attn_kernel(const Prefi
     if (j + 2 < nt) issue(j + 2);
     const int kbuf = j % 3, vbuf = j % 4;
     f32x16_pf st[2];
+    // A wavefront raises its issue priority for its MFMA phases, so that where both wavefronts of a SIMD are
+    // ready the one feeding the matrix core goes first and the other's softmax fills in behind it.
     if (!lag) {
       u32x4 pb[4];
+      __builtin_amdgcn_s_setprio(1);
       qk(kbuf, st);
+      __builtin_amdgcn_s_setprio(0);
       softmax(j, st, pb);
+      __builtin_amdgcn_s_setprio(1);
       pv(vbuf, pb);
+      __builtin_amdgcn_s_setprio(0);
     } else {
+      __builtin_amdgcn_s_setprio(1);
       if (j > 0) pv(vbuf == 0 ? 3 : vbuf - 1, pprev);
       qk(kbuf, st);
+      __builtin_amdgcn_s_setprio(0);
       softmax(j, st, pprev);
     }
   }
