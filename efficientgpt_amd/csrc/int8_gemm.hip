@@ -747,7 +747,7 @@ extern "C" int egpt_int8_gemm_ws(const void* x, int64_t ldx, const int8_t* w, in
       (int64_t)M * ldy * 2 >= ((int64_t)1 << 31) ||
       ((int64_t)M + 63) / 64 * (((int64_t)N + 63) / 64) > (int64_t)INT32_MAX / kMaxSplits)
     return launch_generic((const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, stream);
-  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0, 1, K, nullptr};
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, (uint16_t*)y, ldy, M, N, K, 0, 0, 1, K, nullptr, 0};
   if (workspace) {  // a workspace lets short-M shapes split K
     int splits, kchunk;
     gemm_split(M, N, K, splits, kchunk);
@@ -827,7 +827,8 @@ extern "C" int egpt_int8_gemm_add_rmsnorm(const void* x, int64_t ldx, const int8
   if (!workspace || workspace_bytes < (size_t)splits * (size_t)M * (size_t)N * sizeof(float) ||
       (uintptr_t)workspace % 16)
     return EGPT_ERR_WORKSPACE;
-  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, nullptr, N, M, N, K, 0, 0, splits, kchunk, (float*)workspace};
+  GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, nullptr, N, M, N, K, 0, 0, splits, kchunk, (float*)workspace,
+             0};
   const int st = launch_split_partials(a, stream);
   if (st != EGPT_OK) return st;
   return launch_reduce_add_rmsnorm((const float*)workspace, splits, scale, resid, ld_resid, norm_w, y, ldy, M, N,
@@ -857,7 +858,7 @@ extern "C" int egpt_int8_gemm_qk_norm_rope(const void* x, int64_t ldx, const int
       (uintptr_t)workspace % 16)
     return EGPT_ERR_WORKSPACE;
   GemmArgs a{(const uint16_t*)x, ldx, w, ldw, scale, nullptr, N, M, (int)N, K, 0, 0, splits, kchunk,
-             (float*)workspace};
+             (float*)workspace, 0};
   const int st = launch_split_partials(a, stream);
   if (st != EGPT_OK) return st;
   return launch_reduce_qk_norm_rope((const float*)workspace, splits, scale, positions, q_norm_w, k_norm_w, cos_t,
