@@ -77,6 +77,14 @@ def test_prefill_attention_small_head_dims_and_any_group(d, hq, hkv, rows, cap, 
     _check(q, k, v, hq, hkv, pos0)
 
 
+@pytest.mark.parametrize('d', [32, 64])
+def test_prefill_attention_small_head_dims_long_prompt(d):
+    """Head dims 32 and 64 over a 1000-row prompt that continues 50 filled slots: 17 tiles for the last rows, so
+    the tiles cycle many times through the kernel's K and V buffers at these dims' load counts."""
+    q, k, v, _ = _case(1000, 8, 2, 1100, 50, seed=d + 7, D=d)
+    _check(q, k, v, 8, 2, 50)
+
+
 def test_prefill_attention_qwen3_8b_heads_long_prompt():
     # the Qwen3-8B grouping (32 / 8) over a 2048-token prompt: 32 tiles of 64 slots for the last rows
     q, k, v, _ = _case(2048, 32, 8, 2048, 0, seed=11)
