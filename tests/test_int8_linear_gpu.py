@@ -411,7 +411,8 @@ def test_gemm_add_rmsnorm_matches_the_two_calls_bit_for_bit(m, k, n):
 
 
 @pytest.mark.parametrize('m,k,inter', [(1024, 2048, 6144), (2048, 4096, 12288), (1100, 512, 7000), (128, 2048, 6144),
-                                        (100, 2048, 6144), (200, 2048, 6144), (130, 512, 7000), (40, 4096, 12288)])
+                                        (100, 2048, 6144), (200, 2048, 6144), (130, 512, 7000), (40, 4096, 12288),
+                                        (2048, 192, 4200)])
 def test_gemm_swiglu_matches_the_two_calls_bit_for_bit(m, k, inter):
     """egpt_int8_gemm_swiglu (SwiGLU in the epilogue of the gate/up product, the gate and up rows of a feature
     paired in one wavefront: two column tiles of its large tiles, or the two halves of its one 64 x 64 tile)
@@ -432,6 +433,8 @@ def test_gemm_swiglu_matches_the_two_calls_bit_for_bit(m, k, inter):
                                      inter, k, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(one, two)
-    # 64 rows over 1024 features: the plain product's 32 tiles split K
+    # 64 rows over 1024 features: the plain product's 32 tiles split K where K is a multiple of the 128-wide split
+    # step (refused), and run unsplit otherwise
+    expect = _lib.EGPT_ERR_UNSUPPORTED if k % 128 == 0 else 0
     assert lib.egpt_int8_gemm_swiglu(xd.data_ptr(), k, qd.data_ptr(), k, sd.data_ptr(), one.data_ptr(), inter, 64,
-                                     1024, k, st) == _lib.EGPT_ERR_UNSUPPORTED
+                                     1024, k, st) == expect
